@@ -1,0 +1,71 @@
+import os
+import sys
+
+import pytest
+import torch
+
+_REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+for path in (_REPO, os.path.join(_REPO, "torch-einshard_amd")):
+    if path not in sys.path:
+        sys.path.insert(0, path)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels)")
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """The device for GPU tests; the HIP library must load (no fallback)."""
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device visible")
+    from torch_einshard import _native
+
+    _native.lib()  # raises if libeinshard_hip.so is missing
+    return torch.device("cuda:0")
+
+
+def gen(seed=1234):
+    return torch.Generator().manual_seed(seed)
+
+
+def randn(*shape, seed=1234, dtype=torch.float32, scale=1.0):
+    """Seeded CPU normal draws (fp32, then cast) — the benchmark input recipe."""
+    return (torch.randn(*shape, generator=gen(seed)) * scale).to(dtype)
+
+
+def rel_error(actual, expected):
+    """max |a - e| / max(max|e|, rms(e)): relative error with a scale floor."""
+    a = actual.detach().cpu().to(torch.float64)
+    e = expected.detach().cpu().to(torch.float64)
+    if e.numel() == 0:
+        return 0.0
+    scale = max(e.abs().max().item(), e.pow(2).mean().sqrt().item(), 1e-30)
+    return (a - e).abs().max().item() / scale
+
+
+def assert_rel(actual, expected, tol):
+    assert tuple(actual.shape) == tuple(expected.shape), (tuple(actual.shape), tuple(expected.shape))
+    err = rel_error(actual, expected)
+    assert err <= tol, f"relative error {err:.3e} > {tol:.1e}"
+    return err
+
+
+def assert_bitexact(actual, expected):
+    a = actual.detach().cpu()
+    e = expected.detach().cpu()
+    assert tuple(a.shape) == tuple(e.shape), (tuple(a.shape), tuple(e.shape))
+    assert a.dtype == e.dtype, (a.dtype, e.dtype)
+    if a.numel():
+        av = a.contiguous().view(torch.uint8) if a.element_size() == 1 else a.contiguous().view(
+            {2: torch.int16, 4: torch.int32, 8: torch.int64}[a.element_size()]
+        )
+        ev = e.contiguous().view(torch.uint8) if e.element_size() == 1 else e.contiguous().view(
+            {2: torch.int16, 4: torch.int32, 8: torch.int64}[e.element_size()]
+        )
+        mismatches = (av != ev).sum().item()
+        assert mismatches == 0, f"{mismatches} of {a.numel()} elements differ bitwise"
+
+
+# tolerances stated by the north star: fp32 1e-5 relative, bf16 2e-2 relative
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 5e-3}

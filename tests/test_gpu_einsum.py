@@ -1,0 +1,269 @@
+"""GPU parity of es.einshard against the CPU oracle (the reference's CPU path).
+
+The first block ports every local test of the reference's tests/test_einsum.py
+onto device tensors; the rest sweeps dtypes, layouts, edge sizes and the four
+kernel families.  Tolerances: fp32 1e-5 and bf16 2e-2 relative (with a scale
+floor), bit-exact for copies and single-rounding products."""
+
+import pytest
+import torch
+
+import torch_einshard as es
+from oracle.einshard_oracle import einshard_cpu
+from torch_einshard import _native
+from torch_einshard.symbolic import last_plan
+
+from conftest import TOL, assert_bitexact, assert_rel, randn
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(t, gpu):
+    return t.to(gpu)
+
+
+# ---- reference tests/test_einsum.py, on the GPU ---------------------------------------
+
+
+def test_contract_permute(gpu):
+    x, y = randn(4, 5, 8, 6, seed=333), randn(5, 6, 8, 3, seed=334)
+    z = es.einshard("a b k c, b c l d -> k l d a", dev(x, gpu), dev(y, gpu))
+    assert z.is_cuda
+    assert_rel(z, torch.einsum("abkc,bcld->klda", x, y), 1e-5)
+    assert [step.name for step in last_plan()] == ["rank_local_einsum"]
+
+
+def test_outer(gpu):
+    x, y = randn(3, seed=1), randn(4, seed=2)
+    assert_bitexact(es.einshard("i, j -> i j", dev(x, gpu), dev(y, gpu)), torch.einsum("i,j->ij", x, y))
+
+
+def test_local_einshard_accepts_optimization_policy_arguments(gpu):
+    x, y = dev(randn(3, seed=1), gpu), dev(randn(4, seed=2), gpu)
+    want = torch.einsum("i,j->ij", x.cpu(), y.cpu())
+    assert_bitexact(es.einshard("i, j -> i j", x, y, optimize="memory"), want)
+    assert_bitexact(es.einshard("i, j -> i j", x, y, policy=es.PlanPolicy.from_mode("communication")), want)
+
+
+def test_einshard_rejects_ambiguous_policy_arguments(gpu):
+    with pytest.raises(ValueError, match="either optimize or policy"):
+        es.einshard("i -> i", dev(randn(3), gpu), optimize="memory", policy=es.PlanPolicy.from_mode("training"))
+
+
+def test_optimize_context_applies_to_existing_call_sites(gpu):
+    x, y = dev(randn(3, seed=1), gpu), dev(randn(4, seed=2), gpu)
+    with es.optimize("memory"):
+        z = es.einshard("i, j -> i j", x, y)
+    assert_bitexact(z, torch.einsum("i,j->ij", x.cpu(), y.cpu()))
+
+
+def test_diagonal(gpu):
+    x = randn(5, 5, seed=333)
+    assert_bitexact(es.einshard("i i -> i", dev(x, gpu)), torch.einsum("ii->i", x))
+
+
+def test_ellipsis_contract(gpu):
+    x, w = randn(2, 3, 4, seed=1), randn(4, 5, seed=2)
+    assert_rel(es.einshard("... c, c o -> ... o", dev(x, gpu), dev(w, gpu)), torch.einsum("...c,co->...o", x, w), 1e-5)
+
+
+def test_ellipsis_reduction(gpu):
+    x = randn(2, 3, 4, seed=1)
+    assert_rel(es.einshard("... c -> c", dev(x, gpu)), torch.einsum("...c->c", x), 1e-5)
+
+
+def test_ellipsis_permutation(gpu):
+    x = randn(2, 3, 4, 5, seed=1)
+    assert_bitexact(es.einshard("b ... c -> ... b c", dev(x, gpu)), torch.einsum("b...c->...bc", x))
+
+
+def test_ellipsis_with_factored_axis(gpu):
+    x = randn(2, 3, 12, 5)
+    assert_bitexact(es.einshard("... (h p) c -> ... h p c", dev(x, gpu), sizes={"p": 4}), x.reshape(2, 3, 3, 4, 5))
+
+
+def test_axis_families_window_partition_2d(gpu):
+    x = randn(2, 3, 8, 10, 5)
+    z = es.einshard(
+        "b t [*spatial *window] c -> (b *spatial) t *window c",
+        dev(x, gpu),
+        families={"spatial": ("h", "w"), "window": ("wh", "ww")},
+        sizes={"window": (4, 5)},
+    )
+    expected = x.reshape(2, 3, 2, 4, 2, 5, 5).permute(0, 2, 4, 1, 3, 5, 6).reshape(8, 3, 4, 5, 5)
+    assert_bitexact(z, expected)
+
+
+def test_axis_families_window_partition_3d(gpu):
+    x = randn(2, 3, 8, 10, 6, 5)
+    z = es.einshard(
+        "b t [*spatial *window] c -> (b *spatial) t *window c",
+        dev(x, gpu),
+        families={"spatial": ("h", "w", "d"), "window": ("wh", "ww", "wd")},
+        sizes={"window": (4, 5, 3)},
+    )
+    expected = x.reshape(2, 3, 2, 4, 2, 5, 2, 3, 5).permute(0, 2, 4, 6, 1, 3, 5, 7, 8).reshape(16, 3, 4, 5, 3, 5)
+    assert_bitexact(z, expected)
+
+
+def test_axis_families_window_reverse_3d(gpu):
+    windows = randn(16, 3, 4, 5, 3, 5)
+    z = es.einshard(
+        "(b *spatial) t *window c -> b t [*spatial *window] c",
+        dev(windows, gpu),
+        families={"spatial": ("h", "w", "d"), "window": ("wh", "ww", "wd")},
+        sizes={"b": 2, "h": 2, "w": 2, "d": 2},
+    )
+    expected = windows.reshape(2, 2, 2, 2, 3, 4, 5, 3, 5).permute(0, 4, 1, 5, 2, 6, 3, 7, 8).reshape(2, 3, 8, 10, 6, 5)
+    assert_bitexact(z, expected)
+
+
+def test_axis_family_sizes_expand_by_family_name(gpu):
+    x = randn(2, 12, 5)
+    z = es.einshard("b (*factors) c -> b *factors c", dev(x, gpu), families={"factors": ("h", "p")}, sizes={"factors": (3, 4)})
+    assert_bitexact(z, x.reshape(2, 3, 4, 5))
+
+
+def test_axis_family_rejects_mismatched_zipped_lengths(gpu):
+    with pytest.raises(ValueError, match="matching lengths"):
+        es.einshard(
+            "b t [*spatial *window] c -> b t *spatial *window c",
+            dev(randn(2, 3, 8, 10, 5), gpu),
+            families={"spatial": ("h", "w"), "window": ("wh",)},
+        )
+
+
+def test_expand_factored_axis(gpu):
+    x = randn(2, 12, 5)
+    assert_bitexact(es.einshard("b (h p) c -> b h p c", dev(x, gpu), sizes={"p": 4}), x.reshape(2, 3, 4, 5))
+
+
+def test_pack_factored_axis(gpu):
+    x = randn(2, 3, 4, 5)
+    assert_bitexact(es.einshard("b h p c -> b (h p) c", dev(x, gpu)), x.reshape(2, 12, 5))
+
+
+def test_factored_axis_with_permutation(gpu):
+    x = randn(2, 12, 5)
+    z = es.einshard("b (h p) c -> b c h p", dev(x, gpu), sizes={"h": 3})
+    assert_bitexact(z, x.reshape(2, 3, 4, 5).permute(0, 3, 1, 2))
+
+
+def test_factored_axis_requires_unique_inference(gpu):
+    with pytest.raises(ValueError, match="Cannot infer multiple factor sizes"):
+        es.einshard("b (h p) c -> b h p c", dev(randn(2, 12, 5), gpu))
+
+
+def test_factored_axis_allows_sharded_annotation_locally(gpu):
+    x = randn(2, 12, 5)
+    assert_bitexact(es.einshard("b (h/sp p) c -> b h/sp p c", dev(x, gpu), sizes={"p": 4}), x.reshape(2, 3, 4, 5))
+
+
+def test_factored_axis_rejects_nonlocal_distributed_transform(gpu):
+    with pytest.raises(NotImplementedError, match="local reshape operations"):
+        es.einshard("b (h p) c -> b h/sp p c", dev(randn(2, 12, 5), gpu), sizes={"p": 4})
+
+
+# ---- kernel families across dtypes and layouts -------------------------------------
+
+FAMILY_CASES = [
+    ("a b, b c -> a c", [(70, 45), (45, 90)]),
+    ("a b k c, b c l d -> k l d a", [(16, 4, 24, 16), (4, 16, 24, 8)]),
+    ("b n c, h c -> b n h", [(2, 96, 64), (80, 64)]),
+    ("b i k, b k j -> b i j", [(3, 40, 24), (3, 24, 48)]),
+    ("b i k, b j k -> b j i", [(3, 40, 24), (3, 48, 24)]),
+    ("a b, a b -> a", [(33, 130), (33, 130)]),
+    ("a b, b -> a", [(300, 70), (70,)]),
+    ("p b n h -> b n h", [(4, 3, 20, 64)]),
+    ("b n h -> b h", [(3, 50, 72)]),
+    ("b n h -> b n", [(3, 50, 72)]),
+    ("b n h, h -> b n h", [(3, 20, 64), (64,)]),
+    ("i, j -> i j", [(30,), (41,)]),
+    ("a b c -> c a b", [(5, 6, 7)]),
+    ("i i j, j -> i", [(6, 6, 9), (9,)]),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("expression, shapes", FAMILY_CASES)
+def test_family_parity(gpu, expression, shapes, dtype):
+    xs = [randn(*s, seed=7 + i, dtype=dtype) for i, s in enumerate(shapes)]
+    got = es.einshard(expression, *[dev(x, gpu) for x in xs])
+    want = einshard_cpu(expression, *[x.float() for x in xs]).to(dtype)
+    assert got.dtype == dtype
+    assert_rel(got, want, TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("expression, shapes", FAMILY_CASES)
+def test_family_parity_on_transposed_buffers(gpu, expression, shapes, dtype):
+    xs = []
+    for i, shape in enumerate(shapes):
+        base = randn(*reversed(shape), seed=50 + i, dtype=dtype).to(gpu)
+        xs.append(base.permute(*reversed(range(len(shape)))))
+    got = es.einshard(expression, *xs)
+    want = einshard_cpu(expression, *[x.cpu().float() for x in xs]).to(dtype)
+    assert_rel(got, want, TOL[dtype])
+
+
+GEMM_SHAPES = [(256, 256, 64), (512, 384, 256), (100, 130, 70), (33, 64, 192), (1000, 48, 512), (64, 2048, 128)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("layout", ["nt", "nn", "tn", "tt"])
+@pytest.mark.parametrize("m, n, k", GEMM_SHAPES)
+def test_gemm_layouts(gpu, m, n, k, layout, dtype):
+    x = randn(m, k, seed=m + k, dtype=dtype)
+    w = randn(n, k, seed=n + 3 * k, dtype=dtype)
+    xd, wd = x.to(gpu), w.to(gpu)
+    if layout[0] == "t":
+        xd = x.t().contiguous().to(gpu).t()  # M contiguous
+    if layout[1] == "n":
+        wd = w.t().contiguous().to(gpu).t()  # N contiguous
+    got = es.einshard("m k, n k -> m n", xd, wd)
+    want = einshard_cpu("m k, n k -> m n", x.float(), w.float()).to(dtype)
+    assert_rel(got, want, TOL[dtype])
+
+
+def test_gemm_uses_fast_layouts(gpu):
+    x = randn(512, 256, dtype=torch.bfloat16).to(gpu)
+    w = randn(384, 256, dtype=torch.bfloat16).to(gpu)
+    es.einshard("m k, n k -> m n", x, w)
+    assert _native.last_kernel().startswith("contract_") and "generic" not in _native.last_kernel()
+
+
+def test_contraction_with_empty_sum_writes_zeros(gpu):
+    x = torch.empty(40, 0, device=gpu)
+    y = torch.empty(0, 24, device=gpu)
+    z = es.einshard("a b, b c -> a c", x, y)
+    assert z.shape == (40, 24) and torch.count_nonzero(z).item() == 0
+
+
+def test_empty_output(gpu):
+    x = torch.empty(0, 5, device=gpu)
+    y = torch.empty(5, 3, device=gpu)
+    assert es.einshard("a b, b c -> a c", x, y).shape == (0, 3)
+
+
+def test_copies_are_bitexact_for_integer_and_double(gpu):
+    for dtype in (torch.int32, torch.int64, torch.float64, torch.uint8, torch.int16):
+        x = (randn(3, 4, 5) * 50).to(dtype)
+        assert_bitexact(es.einshard("a b c -> c a b", x.to(gpu)), x.permute(2, 0, 1))
+
+
+def test_broadcast_product_is_bitexact(gpu):
+    for dtype in (torch.float32, torch.bfloat16, torch.float16):
+        x = randn(6, 40, 64, dtype=dtype, seed=4)
+        s = randn(64, dtype=dtype, seed=5)
+        assert_bitexact(es.einshard("b n h, h -> b n h", x.to(gpu), s.to(gpu)), torch.einsum("bnh,h->bnh", x, s))
+
+
+def test_unsupported_dtype_for_arithmetic(gpu):
+    x = torch.ones(4, 4, dtype=torch.float64, device=gpu)
+    with pytest.raises(NotImplementedError, match="not supported"):
+        es.einshard("a b, b c -> a c", x, x)
+
+
+def test_cpu_tensors_are_refused(gpu):
+    with pytest.raises(RuntimeError, match="device tensors"):
+        es.einshard("a b -> b a", torch.ones(2, 3))

@@ -1,0 +1,203 @@
+"""The lowering, checked on the CPU: the exact descriptors the GPU receives are
+executed by a strided fp64 interpreter (test-only) and compared with the oracle.
+
+This pins the planner — label grouping, stride arithmetic, axis merging,
+operand orientation, ellipsis / diagonal / broadcast handling — independently
+of the kernels, which the GPU tests then hold to the same oracle."""
+
+import pytest
+import torch
+
+from oracle.einshard_oracle import einshard_cpu
+from torch_einshard.einsum import plan_local
+from torch_einshard.families import cached_expand_axis_families
+from torch_einshard.grammar import parse_sharding
+from torch_einshard.planner import BcastOp, ContractOp, EmptyOp, GatherOp, ReduceOp, lower_einsum
+
+from conftest import randn
+
+
+def _view(t, axes, field):
+    sizes = [axis.size for axis in axes]
+    strides = [getattr(axis, field) for axis in axes]
+    return torch.as_strided(t, sizes, strides, t.storage_offset())
+
+
+def interpret(op, xs):
+    """Evaluate a planner op on CPU tensors in fp64 using only its descriptors."""
+    xs = [x.to(torch.float64) if x.is_floating_point() else x for x in xs]
+    if isinstance(op, EmptyOp):
+        return torch.empty(op.out_shape, dtype=torch.float64)
+    if isinstance(op, GatherOp):
+        return _view(xs[0], op.axes, "a").reshape(op.out_shape)
+    if isinstance(op, BcastOp):
+        return (_view(xs[0], op.axes, "a") * _view(xs[1], op.axes, "b")).reshape(op.out_shape)
+    if isinstance(op, ReduceOp):
+        axes = op.keep + op.red
+        term = _view(xs[0], axes, "a")
+        if op.has_y:
+            term = term * _view(xs[1], axes, "b")
+        dims = list(range(len(op.keep), len(axes)))
+        total = term.sum(dim=dims) if dims else term
+        return total.reshape(op.out_shape)
+    if isinstance(op, ContractOp):
+        a, b = (xs[1], xs[0]) if op.swapped else (xs[0], xs[1])
+        av = _view(a, op.batch + op.m + op.k, "a")
+        bv = _view(b, op.batch + op.n + op.k, "b")
+        nb, nm, nn, nk = (len(op.batch), len(op.m), len(op.n), len(op.k))
+        size = lambda axes: int(torch.tensor([x.size for x in axes], dtype=torch.int64).prod().item()) if axes else 1
+        am = av.reshape(size(op.batch), size(op.m), size(op.k))
+        bm = bv.reshape(size(op.batch), size(op.n), size(op.k))
+        c = torch.bmm(am, bm.transpose(1, 2))
+        out = torch.zeros(op.out_shape, dtype=torch.float64)
+        target = torch.as_strided(out, [x.size for x in op.batch + op.m + op.n], [x.c for x in op.batch + op.m + op.n])
+        target.copy_(c.reshape([x.size for x in op.batch + op.m + op.n]))
+        del nb, nm, nn, nk
+        return out
+    raise TypeError(type(op))
+
+
+def _f64_view(x):
+    """The same view (shape, strides, offset) over a float64 copy of x's storage."""
+    if x.dtype == torch.float64:
+        return x
+    count = x.untyped_storage().nbytes() // x.element_size()
+    base = torch.empty(0, dtype=x.dtype).set_(x.untyped_storage(), 0, (count,), (1,))
+    return torch.as_strided(base.to(torch.float64), x.shape, x.stride(), x.storage_offset())
+
+
+def check(expression, *xs, sizes=None, families=None, expect=None):
+    xs = [_f64_view(x) for x in xs]
+    text, sizes = cached_expand_axis_families(expression, sizes, families)
+    shard = parse_sharding(text)
+    op, packed = plan_local(shard, *xs, sizes=sizes)
+    if expect is not None:
+        assert isinstance(op, expect), type(op).__name__
+    got = interpret(op, xs)
+    if packed is not None:
+        got = got.reshape(packed)
+    want = einshard_cpu(text, *[x.to(torch.float64) for x in xs], sizes=sizes)
+    assert tuple(got.shape) == tuple(want.shape)
+    torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
+    return op
+
+
+CASES = [
+    ("a b, b c -> a c", [(24, 20), (20, 32)], ContractOp),
+    ("a b k c, b c l d -> k l d a", [(4, 5, 8, 6), (5, 6, 8, 3)], ContractOp),
+    ("b n c, h c -> b n h", [(2, 24, 16), (20, 16)], ContractOp),
+    ("b i k, b k j -> b i j", [(3, 17, 9), (3, 9, 18)], ContractOp),
+    ("b i k, b j k -> b j i", [(3, 17, 9), (3, 18, 9)], ContractOp),
+    ("a b, c -> a c", [(20, 7), (18,)], ContractOp),
+    ("i i j, j -> i", [(5, 5, 7), (7,)], ReduceOp),
+    ("a b, a b -> a", [(9, 13), (9, 13)], ReduceOp),
+    ("a b, b -> a", [(30, 13), (13,)], ReduceOp),
+    ("p b n h -> b n h", [(3, 2, 5, 8)], ReduceOp),
+    ("b n h -> b h", [(2, 5, 8)], ReduceOp),
+    ("b n h -> b n", [(2, 5, 8)], ReduceOp),
+    ("a b c -> b", [(3, 4, 5)], ReduceOp),
+    ("b n h, h -> b n h", [(2, 5, 8), (8,)], BcastOp),
+    ("i, j -> i j", [(3,), (4,)], BcastOp),
+    ("a, a -> a", [(7,), (7,)], BcastOp),
+    ("a b, c d -> d b c a", [(2, 3), (4, 5)], BcastOp),
+    ("i i -> i", [(5, 5)], GatherOp),
+    ("a b c -> c b a", [(3, 4, 5)], GatherOp),
+    ("b t c h w -> b t h w c", [(2, 3, 4, 5, 6)], GatherOp),
+    ("... c, c o -> ... o", [(2, 9, 4), (4, 20)], ContractOp),
+    ("... c, c o -> ... o", [(2, 3, 4), (4, 5)], ReduceOp),
+    ("... c -> c", [(2, 3, 4)], ReduceOp),
+    ("b ... c -> ... b c", [(2, 3, 4, 5)], GatherOp),
+    ("a b -> a b", [(6, 7)], GatherOp),
+]
+
+
+@pytest.mark.parametrize("expression, shapes, kind", CASES)
+def test_planner_matches_oracle(expression, shapes, kind):
+    xs = [randn(*shape, seed=11 + i) for i, shape in enumerate(shapes)]
+    check(expression, *xs, expect=kind)
+
+
+@pytest.mark.parametrize("expression, shapes, kind", CASES)
+def test_planner_on_permuted_inputs(expression, shapes, kind):
+    # non-contiguous operands: a transposed buffer viewed back to the logical shape
+    xs = []
+    for i, shape in enumerate(shapes):
+        base = randn(*reversed(shape), seed=40 + i)
+        xs.append(base.permute(*reversed(range(len(shape)))))
+    check(expression, *xs, expect=kind)
+
+
+def test_planner_with_expanded_operand():
+    x = randn(1, 6, seed=3).expand(5, 6)  # stride 0 along a
+    w = randn(6, 4, seed=4)
+    check("a b, b c -> a c", x, w)
+    check("a b -> b", x)
+    check("a b, b -> a b", x, randn(6, seed=5))
+
+
+def test_planner_size_one_broadcast_and_sliced_operand():
+    x = randn(4, 1, 6, seed=3)
+    y = randn(4, 5, 6, seed=4)
+    check("a b c, a b c -> a b c", x, y)
+    big = randn(10, 12, seed=7)
+    check("a b, b c -> a c", big[1:9:2, 2:10], randn(8, 3, seed=8))
+
+
+def test_planner_factored_and_family_forms():
+    check("b (h p) c -> b h p c", randn(2, 12, 5), sizes={"p": 4})
+    check("b h p c -> b (h p) c", randn(2, 3, 4, 5))
+    check("b (h p) c -> b c h p", randn(2, 12, 5), sizes={"h": 3})
+    check("... (h p) c -> ... h p c", randn(2, 3, 12, 5), sizes={"p": 4})
+    families = {"spatial": ("h", "w"), "window": ("wh", "ww")}
+    check(
+        "b t [*spatial *window] c -> (b *spatial) t *window c",
+        randn(2, 3, 8, 10, 5),
+        families=families,
+        sizes={"window": (4, 5)},
+    )
+
+
+def test_contraction_orientation_puts_contiguous_output_axis_in_n():
+    x = randn(64, 32, 128, 64)
+    y = randn(32, 64, 128, 16)
+    shard = parse_sharding("a b k c, b c l d -> k l d a")
+    op, _ = plan_local(shard, x, y)
+    assert isinstance(op, ContractOp) and op.swapped
+    assert op.n[-1].c == 1 and op.n[-1].size == 64  # output's innermost axis a
+    assert [(ax.size, ax.a) for ax in op.m] == [(2048, 1)]  # (l d) merged, contiguous in y
+    assert [(ax.size, ax.b) for ax in op.k] == [(32, 8192), (64, 1)]  # K contiguous in x
+
+
+def test_config4_lowers_to_one_nt_gemm():
+    x = torch.empty(8, 2048, 4096, device="meta")
+    w = torch.empty(1792, 4096, device="meta")
+    op = lower_einsum([list("abc"), list("dc")], [x.shape, w.shape], [x.stride(), w.stride()], list("abd"))
+    assert isinstance(op, ContractOp) and not op.swapped and not op.batch
+    assert [(a.size, a.a, a.c) for a in op.m] == [(16384, 4096, 1792)]
+    assert [(a.size, a.b, a.c) for a in op.n] == [(1792, 4096, 1)]
+    assert [(a.size, a.a, a.b) for a in op.k] == [(4096, 1, 1)]
+
+
+@pytest.mark.parametrize(
+    "labels, shapes, out, message",
+    [
+        ([list("ab")], [(3,)], list("a"), "does not match the number of dimensions"),
+        ([list("ii")], [(3, 4)], list("i"), "repeated for operand 0"),
+        ([list("a"), list("a")], [(3,), (4,)], list("a"), "do not broadcast"),
+        ([list("a")], [(3,)], list("aa"), "appears more than once"),
+        ([list("a")], [(3,)], list("b"), "does not appear in the equation"),
+    ],
+)
+def test_einsum_errors_match_torch_wording(labels, shapes, out, message):
+    strides = [torch.empty(s).stride() for s in shapes]
+    with pytest.raises(RuntimeError, match=message):
+        lower_einsum(labels, shapes, strides, out)
+
+
+def test_zero_sized_operands():
+    op = lower_einsum([list("ab"), list("bc")], [(0, 3), (3, 4)], [(3, 1), (4, 1)], list("ac"))
+    assert isinstance(op, EmptyOp) and op.out_shape == (0, 4)
+    # an empty summed axis leaves zeros: the kernels receive K = 0
+    op = lower_einsum([list("ab"), list("bc")], [(20, 0), (0, 24)], [(1, 1), (24, 1)], list("ac"))
+    assert isinstance(op, ContractOp) and [a.size for a in op.k] == [0]
+    assert interpret(op, [torch.empty(20, 0), torch.empty(0, 24)]).abs().sum() == 0

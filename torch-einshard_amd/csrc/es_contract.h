@@ -1,0 +1,64 @@
+// es_contract kernels: batched GEMM on gfx950 MFMA over strided label groups.
+//
+//   C[batch, m, n] = sum_k A[batch, m, k] * B[batch, n, k]
+//
+// Every group (batch, M, N, K) is a list of sub-axes with their own strides, so
+// a permuted operand such as x[a,b,k,c] with M = (k, a) and K = (b, c) is read
+// in place: the tile loaders turn a tile index into addresses, no transposed
+// copy is ever materialised.
+//
+// Work-group: WM x WN waves own a BM x BN output tile; the K loop walks BK-deep
+// slabs through double-buffered LDS (one barrier per slab).  LDS keeps both
+// tiles K-contiguous ([row][k], row pitch BK + 16 bytes) so one 16-byte
+// ds_read per lane feeds one MFMA fragment:
+//   * bf16/f16: v_mfma_f32_32x32x16 — lane l holds k = 8*(l/32) .. +7 of row l%32;
+//   * f32:      v_mfma_f32_32x32x2  — a 16-byte read gives a lane 4 consecutive
+//     k; four MFMAs consume them, lanes 0-31 supplying k 0..3 and lanes 32-63
+//     k 4..7.  Both operands use the same k assignment, so every product
+//     A[m,k]*B[n,k] is formed exactly once (only the summation order differs).
+// The MFMA's first operand is the N-side fragment and the second the M-side
+// one, so the accumulator holds C^T: each lane ends with 4 consecutive n of
+// one m.  The epilogue stages 32-row slices of the tile in LDS and writes
+// them with 16-byte stores along n when n is the output's contiguous axis.
+//
+// Global -> LDS loaders (per operand):
+//   * K-contiguous: 16-byte loads along k, stored as-is;
+//   * MN-contiguous: a thread loads a VEC(k) x VEC(m) block with 16-byte loads
+//     along m and transposes it in registers (v_perm_b32 for 16-bit types)
+//     before 16-byte LDS stores;
+//   * generic: element loads with full index decomposition (any strides).
+#pragma once
+
+#include "es_common.h"
+
+namespace es {
+
+enum OperandLayout { kKContig = 0, kMNContig = 1, kGeneric = 2 };
+
+struct GroupArgs {
+  int32_t n;
+  FastDiv div[ES_MAX_AXES];
+  int64_t sa[ES_MAX_AXES];
+  int64_t sb[ES_MAX_AXES];
+  int64_t sc[ES_MAX_AXES];
+};
+
+struct ContractArgs {
+  const void* a;
+  const void* b;
+  void* c;
+  uint32_t M, N, K, batch;
+  uint32_t tiles_m, tiles_n;
+  uint32_t total_tiles;
+  int32_t vstore;        // 16-byte vector stores along n
+  int64_t ka_inner;      // stride of the innermost K sub-axis in A
+  int64_t kb_inner;      // ... in B
+  GroupArgs gb, gm, gn, gk;
+};
+
+// Launch one contraction; `config` 0 = 256x256, 1 = 128x128, 2 = 64x64.
+int launch_contract_f32(const ContractArgs& p, int config, int la, int lb, hipStream_t s);
+int launch_contract_bf16(const ContractArgs& p, int config, int la, int lb, hipStream_t s);
+int launch_contract_f16(const ContractArgs& p, int config, int la, int lb, hipStream_t s);
+
+}  // namespace es

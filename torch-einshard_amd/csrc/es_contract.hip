@@ -1,0 +1,136 @@
+// es_contract entry point: descriptor validation, operand-layout and tile
+// selection, launch.
+#include "es_contract.h"
+
+#include <string>
+
+namespace es {
+namespace {
+
+constexpr int kMax = ES_MAX_AXES;
+
+int fill_group(GroupArgs& g, int n, const es_axis* axes, uint64_t& extent, const char* name) {
+  if (n < 0 || n > kMax) return fail(ES_ERR_INVALID, std::string("es_contract: too many ") + name + " axes");
+  g.n = n;
+  extent = 1;
+  for (int i = 0; i < kMax; ++i) {
+    if (i < n) {
+      if (axes[i].size < 0) return fail(ES_ERR_INVALID, std::string("es_contract: negative ") + name + " size");
+      extent *= uint64_t(axes[i].size);
+      if (uint64_t(axes[i].size) > kU32Max) return fail(ES_ERR_UNSUPPORTED, "es_contract: axis too large");
+      g.div[i].init(uint32_t(axes[i].size));
+      g.sa[i] = axes[i].a;
+      g.sb[i] = axes[i].b;
+      g.sc[i] = axes[i].c;
+    } else {
+      g.div[i].init(1);
+      g.sa[i] = g.sb[i] = g.sc[i] = 0;
+    }
+  }
+  if (extent > kU32Max) return fail(ES_ERR_UNSUPPORTED, std::string("es_contract: ") + name + " extent >= 2^32");
+  return ES_OK;
+}
+
+bool strides_multiple(const es_axis* axes, int n, int skip_last, int which, int64_t q) {
+  for (int i = 0; i < n - skip_last; ++i) {
+    const int64_t s = which == 0 ? axes[i].a : (which == 1 ? axes[i].b : axes[i].c);
+    if (s % q != 0) return false;
+  }
+  return true;
+}
+
+// layout of one operand: `which` 0 = A (rows = M), 1 = B (rows = N)
+int operand_layout(const es_contract_desc* d, const void* ptr, int which, int vec, int bk) {
+  const es_axis* rows = which == 0 ? d->m : d->n;
+  const int nrows = which == 0 ? d->n_m : d->n_n;
+  if (!aligned(ptr, 16) || d->n_k == 0) return kGeneric;
+  const es_axis& kin = d->k[d->n_k - 1];
+  const int64_t kin_stride = which == 0 ? kin.a : kin.b;
+  if (kin.size % bk != 0) return kGeneric;
+  const bool batch_ok = strides_multiple(d->batch, d->n_batch, 0, which, vec);
+  if (!batch_ok) return kGeneric;
+  if (kin_stride == 1 && strides_multiple(d->k, d->n_k, 1, which, vec) &&
+      strides_multiple(rows, nrows, 0, which, vec))
+    return kKContig;
+  if (nrows > 0) {
+    const es_axis& rin = rows[nrows - 1];
+    const int64_t rin_stride = which == 0 ? rin.a : rin.b;
+    if (rin_stride == 1 && rin.size % vec == 0 && strides_multiple(rows, nrows, 1, which, vec) &&
+        strides_multiple(d->k, d->n_k, 0, which, vec))
+      return kMNContig;
+  }
+  return kGeneric;
+}
+
+}  // namespace
+}  // namespace es
+
+extern "C" int es_contract(const es_contract_desc* d, const void* a, const void* b, void* c, void* stream) {
+  using namespace es;
+  if (d == nullptr) return fail(ES_ERR_INVALID, "es_contract: null descriptor");
+  const int esz = dtype_size(d->dtype);
+  if (esz == 0) return fail(ES_ERR_UNSUPPORTED, "es_contract: unsupported dtype");
+
+  ContractArgs p;
+  uint64_t nb, nm, nn, nk;
+  int st;
+  if ((st = fill_group(p.gb, d->n_batch, d->batch, nb, "batch")) != ES_OK) return st;
+  if ((st = fill_group(p.gm, d->n_m, d->m, nm, "m")) != ES_OK) return st;
+  if ((st = fill_group(p.gn, d->n_n, d->n, nn, "n")) != ES_OK) return st;
+  if ((st = fill_group(p.gk, d->n_k, d->k, nk, "k")) != ES_OK) return st;
+  if (nb * nm * nn == 0) return ES_OK;
+  if (a == nullptr || b == nullptr || c == nullptr) return fail(ES_ERR_INVALID, "es_contract: null pointer");
+  if (nk > uint64_t(0x7fffffff)) return fail(ES_ERR_UNSUPPORTED, "es_contract: K too large");
+
+  const int vec = 16 / esz;
+  const int bk = esz == 4 ? 32 : 64;
+  int la = operand_layout(d, a, 0, vec, bk);
+  int lb = operand_layout(d, b, 1, vec, bk);
+  if (nk == 0) la = lb = kGeneric;  // nothing to load: the generic kernel writes zeros
+
+  p.a = a;
+  p.b = b;
+  p.c = c;
+  p.M = uint32_t(nm);
+  p.N = uint32_t(nn);
+  p.K = uint32_t(nk);
+  p.batch = uint32_t(nb);
+  p.ka_inner = d->n_k > 0 ? d->k[d->n_k - 1].a : 0;
+  p.kb_inner = d->n_k > 0 ? d->k[d->n_k - 1].b : 0;
+  p.vstore = 0;
+  if (d->n_n > 0) {
+    const es_axis& nin = d->n[d->n_n - 1];
+    if (nin.c == 1 && nin.size % vec == 0 && aligned(c, 16) && strides_multiple(d->n, d->n_n, 1, 2, vec) &&
+        strides_multiple(d->m, d->n_m, 0, 2, vec) && strides_multiple(d->batch, d->n_batch, 0, 2, vec))
+      p.vstore = 1;
+  }
+
+  // tile: the largest that still gives every CU a tile of its own
+  static const int tile_of[3] = {256, 128, 64};
+  int config = 2;
+  if (la != kGeneric && lb != kGeneric) {
+    for (int cfg = 0; cfg < 3; ++cfg) {
+      const uint64_t t = uint64_t(tile_of[cfg]);
+      const uint64_t tiles = ((nm + t - 1) / t) * ((nn + t - 1) / t) * nb;
+      if (tiles >= 256 || cfg == 2) {
+        config = cfg;
+        break;
+      }
+    }
+  }
+  const uint64_t t = uint64_t(tile_of[config]);
+  const uint64_t tm = (nm + t - 1) / t, tn = (nn + t - 1) / t;
+  const uint64_t total = tm * tn * nb;
+  if (total > uint64_t(0x7fffffff)) return fail(ES_ERR_UNSUPPORTED, "es_contract: too many tiles");
+  p.tiles_m = uint32_t(tm);
+  p.tiles_n = uint32_t(tn);
+  p.total_tiles = uint32_t(total);
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (d->dtype) {
+    case ES_F32: return launch_contract_f32(p, config, la, lb, s);
+    case ES_BF16: return launch_contract_bf16(p, config, la, lb, s);
+    case ES_F16: return launch_contract_f16(p, config, la, lb, s);
+  }
+  return fail(ES_ERR_UNSUPPORTED, "es_contract: unsupported dtype");
+}

@@ -1,0 +1,169 @@
+"""torch_einshard — MI355X (gfx950) build of torch-einshard's single-device path.
+
+Public surface kept from the reference (src/torch_einshard/__init__.py:1-57,
+346-372): ``einshard``, ``einshard_like``, ``einwindow``, ``einhalo``, the
+notation types, ``PlanPolicy`` / ``optimize`` and the plan diagnostics.
+Arithmetic runs on hand-written HIP kernels (libeinshard_hip.so) on ROCm
+device tensors; there is no CPU path and no fallback to ``torch.einsum``.
+"""
+
+from . import symbolic
+from .distributed import distributed_1d
+from .einsum import einsum, equation_of
+from .families import cached_expand_axis_families
+from .grammar import Axes, parse_sharding
+from .halo import einhalo, einwindow
+from .sharding import Axis, AxisGroup, EllipsisAxis, TensorAnnotation, TensorSpec
+from .symbolic import (
+    ExecutionPlan,
+    PlanPolicy,
+    get_default_policy,
+    get_optimization_policy,
+    last_alternatives,
+    last_candidates,
+    last_plan,
+    optimize,
+    resolve_plan_policy,
+    set_default_policy,
+    set_last_plan,
+)
+
+__all__ = [
+    "einshard",
+    "einshard_like",
+    "einwindow",
+    "einhalo",
+    "einsum",
+    "equation_of",
+    "parse_sharding",
+    "local_operation",
+    "Axes",
+    "Axis",
+    "AxisGroup",
+    "EllipsisAxis",
+    "TensorAnnotation",
+    "TensorSpec",
+    "ExecutionPlan",
+    "PlanPolicy",
+    "optimize",
+    "resolve_plan_policy",
+    "set_default_policy",
+    "get_default_policy",
+    "get_optimization_policy",
+    "set_last_plan",
+    "last_plan",
+    "last_candidates",
+    "last_alternatives",
+]
+
+__version__ = "0.1.0"
+
+
+def _axes(spec):
+    return spec.axes if hasattr(spec, "axes") else spec
+
+
+def _flat(spec):
+    axes = _axes(spec)
+    return axes.flat() if hasattr(axes, "flat") else axes
+
+
+def _has_groups(spec):
+    return any(isinstance(axis, AxisGroup) for axis in _axes(spec))
+
+
+def local_operation(shard):
+    """True when the expression needs no communication (reference __init__.py:90-120)."""
+    if any(getattr(spec, "partials", ()) for spec in shard if spec is not None):
+        return False
+    if shard[1] is None:
+        return Axes(set(_flat(shard[0])) ^ set(_flat(shard[2]))).local()
+    x_axes = list(_flat(shard[0]))
+    y_axes = list(_flat(shard[1]))
+    inputs = x_axes + y_axes
+    for axis in _flat(shard[2]):
+        if axis in inputs:
+            continue
+        if any(other.name == axis.name for other in inputs):
+            return False
+    x_by_name = {axis.name: axis for axis in x_axes}
+    y_by_name = {axis.name: axis for axis in y_axes}
+    for name in set(x_by_name) & set(y_by_name):
+        a, b = x_by_name[name], y_by_name[name]
+        if not a.local() or not b.local() or a != b:
+            return False
+    return True
+
+
+def _distributed_einshard(shard, xs, mesh, shapes, policy):
+    if any(_has_groups(spec) for spec in shard if spec is not None):
+        raise NotImplementedError("Factored axes are currently supported only for local reshape operations")
+    if mesh is None:
+        raise ValueError("Distributed einshard operations require mesh")
+    return distributed_1d(shard, *xs, mesh=mesh, shapes=shapes, policy=policy)
+
+
+def _execute_einshard(shard, xs, mesh, shapes, sizes, policy):
+    if local_operation(shard):
+        output = einsum(shard, *xs, sizes=sizes)
+        plan = ExecutionPlan()
+        plan.add("rank_local_einsum")
+        set_last_plan(plan)
+        return output
+    return _distributed_einshard(shard, xs, mesh, shapes, policy)
+
+
+def einshard(shard, *xs, mesh=None, shapes=None, sizes=None, families=None, optimize=None, policy=None):
+    """Evaluate an einshard expression, e.g. ``einshard("b n c, h c -> b n h", x, w)``.
+
+    Mirrors the reference entry point (src/torch_einshard/__init__.py:346-354):
+    resolve the plan policy, expand axis families, parse, then run the local
+    einsum or — for partial / resharding expressions — the mesh path.
+    ``[param]`` operand annotations are parsed and validated; attaching
+    parameter-layout metadata to tensors is not part of this build.
+    """
+    policy = resolve_plan_policy(optimize=optimize, policy=policy)
+    shard, sizes = cached_expand_axis_families(shard, sizes, families)
+    shard = parse_sharding(shard)
+    return _execute_einshard(shard, xs, mesh, shapes, sizes, policy)
+
+
+def einshard_like(shard, *xs, mesh=None, sizes=None, families=None):
+    """Parse and validate ``shard`` like ``einshard`` without running it; returns ``None``.
+
+    The reference also registers ``[param]`` metadata here (reference
+    __init__.py:357-372); this build validates the expression only.
+    """
+    shard, _ = cached_expand_axis_families(shard, sizes, families)
+    shard = parse_sharding(shard)
+    if local_operation(shard):
+        for spec in (shard[0], shard[1]):
+            if spec is not None and getattr(spec, "partials", ()):
+                raise ValueError("Local einsum does not support partial inputs")
+        _validate_output_axes(shard, exact=True)
+        return None
+    _validate_output_axes(shard, exact=False)
+    if any(_has_groups(spec) for spec in shard if spec is not None):
+        raise NotImplementedError("Factored axes are currently supported only for local reshape operations")
+    if mesh is None:
+        raise ValueError("Distributed einshard operations require mesh")
+    return None
+
+
+def _validate_output_axes(shard, *, exact):
+    def key(axis):
+        return axis if exact else axis.name
+
+    inputs = {key(axis) for axis in _flat(shard[0]) if not isinstance(axis, EllipsisAxis)}
+    if shard[1] is not None:
+        inputs.update(key(axis) for axis in _flat(shard[1]) if not isinstance(axis, EllipsisAxis))
+    seen = set()
+    for axis in _flat(shard[2]):
+        if isinstance(axis, EllipsisAxis):
+            continue
+        k = key(axis)
+        if k in seen:
+            raise ValueError(f"Output dimension {axis} appears more than once")
+        seen.add(k)
+        if k not in inputs:
+            raise ValueError(f"Output dimension {axis} must be present in input")
