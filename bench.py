@@ -1,0 +1,352 @@
+"""Benchmark of torch_einshard's MI355X path (one JSON line per workload).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c1|c2|c3|c5a|c5b|c5c|all]
+
+A step is one es.einshard / es.einwindow call over one batch of synthetic
+input that is already resident in HBM.  The default workload is config 4 of
+BASELINE.json — one rank's share of a tensor-parallel contraction,
+es.einshard("b n c, h c -> b n h") with x[8,2048,4096], w[1792,4096] bf16 —
+the configuration the north star's headline target (>= 70 % of bf16 MFMA peak)
+is quoted on.  The other configs are parity cases; ``--workload`` measures them
+individually with the same method.
+
+Timing: W untimed warm-up steps, then K steps between two device
+synchronisations (wall clock -> ms_per_step) with HIP events recorded on the
+stream the kernel runs on (torch's current stream, which the library launches
+on) -> the kernel's average duration.  HBM-bound workloads write a 512 MiB
+buffer between steps so their inputs are not served from the 256 MB Infinity
+Cache; those steps are timed one by one with events (the flush is not timed).
+
+roofline.achieved uses algorithmic work only: 2*M*N*K flops for contractions,
+unique input bytes + output bytes for the copy / reduce / broadcast kernels.
+cpu_baseline times the reference's CPU path as restated by oracle/ on the host
+cores (torch.einsum / F.pad + unfold + permute on CPU tensors) on a bounded
+sample of the same workload, scaled to the same unit.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+_REPO = os.path.dirname(os.path.abspath(__file__))
+for _path in (os.path.join(_REPO, "torch-einshard_amd"), _REPO):
+    if _path not in sys.path:
+        sys.path.insert(0, _path)
+
+import torch  # noqa: E402
+
+METRIC = "einshard contraction TFLOP/s; einwindow/reduce GB/s; % of MI355X roofline"
+PEAK = {
+    "bf16": 2500.0,  # TFLOP/s, dense MFMA
+    "f16": 2500.0,
+    "f32": 157.3,  # TFLOP/s, fp32 MFMA
+    "hbm": 8000.0,  # GB/s
+}
+SEED = 1234
+
+
+def _gen():
+    return torch.Generator().manual_seed(SEED)
+
+
+# ---- workloads ---------------------------------------------------------------------------
+# each returns dict(name, call(inputs)->out, inputs, flops|bytes, unit, bound, dtype, cpu)
+
+
+def wl_c1(dev):
+    g = _gen()
+    x = torch.randn(1024, 1024, generator=g)
+    y = torch.randn(1024, 1024, generator=g)
+    return dict(
+        key="c1",
+        workload="config1: es.einshard('a b, b c -> a c') x,y [1024,1024] fp32",
+        expr="a b, b c -> a c",
+        host=[x, y],
+        flops=2 * 1024**3,
+        dtype="f32",
+        bound="mfma",
+        peak=PEAK["f32"],
+        sample=lambda xs: ([xs[0], xs[1]], 1.0),
+    )
+
+
+def wl_c2(dev):
+    g = _gen()
+    x = torch.randn(64, 32, 128, 64, generator=g).to(torch.bfloat16)
+    y = torch.randn(32, 64, 128, 16, generator=g).to(torch.bfloat16)
+    return dict(
+        key="c2",
+        workload="config2: es.einshard('a b k c, b c l d -> k l d a') a=64 b=32 k=128 c=64 l=128 d=16 bf16",
+        expr="a b k c, b c l d -> k l d a",
+        host=[x, y],
+        flops=2 * 8192 * 2048 * 2048,
+        dtype="bf16",
+        bound="mfma",
+        peak=PEAK["bf16"],
+        sample=lambda xs: ([xs[0][:8], xs[1]], 8 / 64),
+    )
+
+
+def wl_c4(dev):
+    g = _gen()
+    x = (torch.randn(8, 2048, 4096, generator=g) * 0.02).to(torch.bfloat16)
+    w = (torch.randn(1792, 4096, generator=g) * 0.02).to(torch.bfloat16)
+    return dict(
+        key="c4",
+        workload="config4: es.einshard('b n c, h c -> b n h') x[8,2048,4096] w[1792,4096] bf16 (one TP rank's share)",
+        expr="b n c, h c -> b n h",
+        host=[x, w],
+        flops=2 * 16384 * 1792 * 4096,
+        dtype="bf16",
+        bound="mfma",
+        peak=PEAK["bf16"],
+        sample=lambda xs: ([xs[0][:1, :512], xs[1]], 512 / 16384),
+    )
+
+
+def wl_c3(dev):
+    g = _gen()
+    x = torch.randn(8, 256, 256, 64, generator=g).to(torch.bfloat16)
+    return dict(
+        key="c3",
+        workload="config3: es.einwindow('b h w c -> b h w kh kw c', {h:kh, w:kw}, {h:1, w:1}) x[8,256,256,64] bf16",
+        window=("b h w c -> b h w kh kw c", {"h": "kh", "w": "kw"}, {"h": 1, "w": 1}),
+        host=[x],
+        bytes=8 * 256 * 256 * 64 * 2 + 8 * 256 * 256 * 9 * 64 * 2,
+        dtype="bf16",
+        bound="hbm",
+        peak=PEAK["hbm"],
+        sample=lambda xs: ([xs[0][:1]], 1 / 8),
+    )
+
+
+def _c5_input():
+    g = _gen()
+    return torch.rand(8, 16, 4096, 4096, generator=g) * 2 - 1
+
+
+def wl_c5a(dev):
+    x = _c5_input()
+    return dict(
+        key="c5a",
+        workload="config5a: es.einshard('p b n h -> b n h') P=8 b=16 n=h=4096 fp32",
+        expr="p b n h -> b n h",
+        host=[x],
+        bytes=8 * 16 * 4096 * 4096 * 4 + 16 * 4096 * 4096 * 4,
+        dtype="f32",
+        bound="hbm",
+        peak=PEAK["hbm"],
+        sample=lambda xs: ([xs[0][:, :1]], 1 / 16),
+    )
+
+
+def wl_c5b(dev):
+    g = _gen()
+    y = torch.rand(16, 4096, 4096, generator=g) * 2 - 1
+    s = torch.rand(4096, generator=g) * 2 - 1
+    return dict(
+        key="c5b",
+        workload="config5b: es.einshard('b n h, h -> b n h') b=16 n=h=4096 fp32",
+        expr="b n h, h -> b n h",
+        host=[y, s],
+        bytes=2 * 16 * 4096 * 4096 * 4 + 4096 * 4,
+        dtype="f32",
+        bound="hbm",
+        peak=PEAK["hbm"],
+        sample=lambda xs: ([xs[0][:2], xs[1]], 2 / 16),
+    )
+
+
+def wl_c5c(dev):
+    g = _gen()
+    z = torch.rand(16, 4096, 4096, generator=g) * 2 - 1
+    return dict(
+        key="c5c",
+        workload="config5c: es.einshard('b n h -> b h') b=16 n=h=4096 fp32",
+        expr="b n h -> b h",
+        host=[z],
+        bytes=16 * 4096 * 4096 * 4 + 16 * 4096 * 4,
+        dtype="f32",
+        bound="hbm",
+        peak=PEAK["hbm"],
+        sample=lambda xs: ([xs[0][:2]], 2 / 16),
+    )
+
+
+WORKLOADS = {"c1": wl_c1, "c2": wl_c2, "c3": wl_c3, "c4": wl_c4, "c5a": wl_c5a, "c5b": wl_c5b, "c5c": wl_c5c}
+
+
+def _runner(es, wl):
+    if "window" in wl:
+        expr, windows, radius = wl["window"]
+        return lambda xs: es.einwindow(expr, xs[0], windows, radius)
+    expr = wl["expr"]
+    return lambda xs: es.einshard(expr, *xs)
+
+
+def _cpu_runner(wl):
+    from oracle.einshard_oracle import einshard_cpu, einwindow_cpu
+
+    if "window" in wl:
+        expr, windows, radius = wl["window"]
+        return lambda xs: einwindow_cpu(expr, xs[0], windows, radius)
+    expr = wl["expr"]
+    return lambda xs: einshard_cpu(expr, *xs)
+
+
+def measure_gpu(es, wl, dev, steps, warmup):
+    xs = [t.to(dev) for t in wl["host"]]
+    run = _runner(es, wl)
+    flush = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev) if wl["bound"] == "hbm" else None
+    for _ in range(warmup):
+        run(xs)
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    if flush is None:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        start.record(stream)
+        for _ in range(steps):
+            out = run(xs)
+        end.record(stream)
+        torch.cuda.synchronize(dev)
+        wall = time.perf_counter() - t0
+        kernel_ms = start.elapsed_time(end) / steps
+    else:
+        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        for s, e in events:
+            flush.fill_(1)
+            s.record(stream)
+            out = run(xs)
+            e.record(stream)
+        torch.cuda.synchronize(dev)
+        wall = time.perf_counter() - t0
+        kernel_ms = sum(s.elapsed_time(e) for s, e in events) / steps
+    from torch_einshard import _native
+
+    kernel_name = _native.last_kernel()
+    del out
+    return dict(wall_s=wall, kernel_ms=kernel_ms, kernel=kernel_name)
+
+
+def measure_cpu(wl, budget_s=12.0):
+    """Time the oracle (reference CPU path) on a bounded sample; returns per-unit rate."""
+    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "64") or 64))
+    torch.set_num_threads(max(threads, 1))
+    run = _cpu_runner(wl)
+    sample, fraction = wl["sample"](wl["host"])
+    sample = [t.contiguous() for t in sample]
+    t0 = time.perf_counter()
+    run(sample)  # warm-up
+    first = time.perf_counter() - t0
+    iters = max(1, min(20, int(budget_s / max(first, 1e-3))))
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        run(sample)
+    per = (time.perf_counter() - t0) / iters
+    work = wl.get("flops", wl.get("bytes")) * fraction
+    if "flops" in wl:
+        value = work / per / 1e12
+        unit = "TFLOP/s"
+    else:
+        value = work / per / 1e9
+        unit = "GB/s"
+    shape = " x ".join(str(list(t.shape)) for t in sample)
+    return dict(
+        value=round(value, 4),
+        unit=unit,
+        cores=torch.get_num_threads(),
+        kind="port",
+        sample=f"{shape} ({fraction:.4g} of the workload), {iters} timed iterations of {per * 1e3:.1f} ms",
+    )
+
+
+def bench_one(es, key, dev, steps, warmup, cpu=True):
+    wl = WORKLOADS[key](dev)
+    g = measure_gpu(es, wl, dev, steps, warmup)
+    ms_per_step = g["wall_s"] * 1e3 / steps
+    if "flops" in wl:
+        value = wl["flops"] / (ms_per_step / 1e3) / 1e12
+        achieved = wl["flops"] / (g["kernel_ms"] / 1e3) / 1e12
+        unit = "TFLOP/s"
+    else:
+        value = wl["bytes"] / (ms_per_step / 1e3) / 1e9
+        achieved = wl["bytes"] / (g["kernel_ms"] / 1e3) / 1e9
+        unit = "GB/s"
+    roofline = dict(
+        bound=wl["bound"],
+        achieved=round(achieved, 2),
+        peak=wl["peak"],
+        unit=unit,
+        frac=round(achieved / wl["peak"], 4),
+        traffic=_traffic(key),
+        kernel=g["kernel"],
+        kernel_ms=round(g["kernel_ms"], 5),
+    )
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": wl["dtype"],
+        "data": f"synthetic (torch.Generator seed {SEED}, generated on CPU, copied to HBM)",
+        "config": {"workload": wl["workload"], "device": torch.cuda.get_device_name(dev)},
+        "roofline": roofline,
+        "cpu_baseline": measure_cpu(wl) if cpu else None,
+    }
+    return line
+
+
+def _traffic(key):
+    """HBM bytes per launch measured with rocprofv3 counters (profiles/traffic.json), else None."""
+    path = os.path.join(_REPO, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        return json.load(open(path)).get(key, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main(argv=None):
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--workload", default="c4", choices=sorted(WORKLOADS) + ["all"])
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = parser.parse_args(argv)
+    if args.gpus != 1:
+        print(
+            f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+            "(collectives across GPUs are not part of it)",
+            file=sys.stderr,
+        )
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm device visible", file=sys.stderr)
+        return 2
+    import torch_einshard as es
+
+    dev = torch.device("cuda:0")
+    keys = sorted(WORKLOADS) if args.workload == "all" else [args.workload]
+    for key in keys:
+        line = bench_one(es, key, dev, args.steps, args.warmup, cpu=not args.no_cpu)
+        print(json.dumps(line), flush=True)
+        torch.cuda.empty_cache()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -79,7 +79,9 @@ extern "C" int es_contract(const es_contract_desc* d, const void* a, const void*
   if ((st = fill_group(p.gn, d->n_n, d->n, nn, "n")) != ES_OK) return st;
   if ((st = fill_group(p.gk, d->n_k, d->k, nk, "k")) != ES_OK) return st;
   if (nb * nm * nn == 0) return ES_OK;
-  if (a == nullptr || b == nullptr || c == nullptr) return fail(ES_ERR_INVALID, "es_contract: null pointer");
+  // an empty K reads nothing (torch hands out null data pointers for empty tensors)
+  if (c == nullptr || (nk > 0 && (a == nullptr || b == nullptr)))
+    return fail(ES_ERR_INVALID, "es_contract: null pointer");
   if (nk > uint64_t(0x7fffffff)) return fail(ES_ERR_UNSUPPORTED, "es_contract: K too large");
 
   const int vec = 16 / esz;

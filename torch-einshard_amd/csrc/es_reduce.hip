@@ -398,7 +398,8 @@ extern "C" int es_reduce(const es_reduce_desc* d, const void* x, const void* y, 
   int st = plan(d, nullptr, nullptr, nullptr, sizing);
   if (st != ES_OK) return st;
   if (sizing.n_out == 0) return ES_OK;
-  if (out == nullptr || x == nullptr || (d->has_y && y == nullptr))
+  // an empty reduced extent reads nothing (torch hands out null pointers for empty tensors)
+  if (out == nullptr || (sizing.n_red > 0 && (x == nullptr || (d->has_y && y == nullptr))))
     return fail(ES_ERR_INVALID, "es_reduce: null pointer");
   Schedule s;
   st = plan(d, x, y, out, s);
