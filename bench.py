@@ -175,7 +175,32 @@ def wl_c5c(dev):
     )
 
 
-WORKLOADS = {"c1": wl_c1, "c2": wl_c2, "c3": wl_c3, "c4": wl_c4, "c5a": wl_c5a, "c5b": wl_c5b, "c5c": wl_c5c}
+def wl_copy(dev):
+    """Calibration: a plain 1 GiB copy through the same gather kernel (known traffic)."""
+    x = torch.empty(16384, 16384, dtype=torch.float32).fill_(1.0)
+    return dict(
+        key="copy",
+        workload="calibration: es.einshard('a b -> a b') x[16384,16384] fp32 (1 GiB read + 1 GiB write)",
+        expr="a b -> a b",
+        host=[x],
+        bytes=2 * 16384 * 16384 * 4,
+        dtype="f32",
+        bound="hbm",
+        peak=PEAK["hbm"],
+        sample=lambda xs: ([xs[0][:1024]], 1 / 16),
+    )
+
+
+WORKLOADS = {
+    "c1": wl_c1,
+    "c2": wl_c2,
+    "c3": wl_c3,
+    "c4": wl_c4,
+    "c5a": wl_c5a,
+    "c5b": wl_c5b,
+    "c5c": wl_c5c,
+    "copy": wl_copy,
+}
 
 
 def _runner(es, wl):
@@ -340,7 +365,7 @@ def main(argv=None):
     import torch_einshard as es
 
     dev = torch.device("cuda:0")
-    keys = sorted(WORKLOADS) if args.workload == "all" else [args.workload]
+    keys = [k for k in sorted(WORKLOADS) if k != "copy"] if args.workload == "all" else [args.workload]
     for key in keys:
         line = bench_one(es, key, dev, args.steps, args.warmup, cpu=not args.no_cpu)
         print(json.dumps(line), flush=True)

@@ -68,6 +68,7 @@ typedef struct {
  * If some i_d falls outside [0, in_size[d]) the boundary rule applies (per
  * dim, all dims share the rule); with ES_BOUNDARY_CONSTANT the whole element
  * is `fill`.  Otherwise out[o] = x[sum_d i_d * in_stride[d]].
+ * win[d] is -1 or an output dim other than pos[d].
  * Elements are copied as raw bits (elem_size 1, 2, 4 or 8 bytes): bit-exact. */
 typedef struct {
   int32_t elem_size;

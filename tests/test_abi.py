@@ -71,6 +71,17 @@ def test_bad_descriptors_are_rejected_before_any_launch():
     status, message = _status("es_gather", ctypes.byref(desc), None, None, None)
     assert status == _native.ES_ERR_INVALID and "elem_size" in message
 
+    # an input dim fed twice by the same output dim is not a window
+    desc.elem_size = 2
+    desc.out_rank = 2
+    desc.out_size[0] = desc.out_size[1] = 4
+    desc.in_rank = 1
+    desc.in_size[0] = 8
+    desc.in_stride[0] = 1
+    desc.pos[0] = desc.win[0] = 1
+    status, message = _status("es_gather", ctypes.byref(desc), None, None, None)
+    assert status == _native.ES_ERR_INVALID and "same output dim" in message
+
     cdesc = _native.ContractDesc()
     cdesc.dtype = 7
     status, message = _status("es_contract", ctypes.byref(cdesc), None, None, None, None)

@@ -51,8 +51,11 @@ struct ContractArgs {
   uint32_t tiles_m, tiles_n;
   uint32_t total_tiles;
   int32_t vstore;        // 16-byte vector stores along n
+  uint32_t k_inner;      // extent of the innermost K sub-axis (fast paths: a multiple of BK)
   int64_t ka_inner;      // stride of the innermost K sub-axis in A
   int64_t kb_inner;      // ... in B
+  int64_t ka_outer;      // stride of the outer K sub-axis in A (fast paths have at most two)
+  int64_t kb_outer;      // ... in B
   GroupArgs gb, gm, gn, gk;
 };
 

@@ -85,7 +85,7 @@ extern "C" int es_contract(const es_contract_desc* d, const void* a, const void*
   if (nk > uint64_t(0x7fffffff)) return fail(ES_ERR_UNSUPPORTED, "es_contract: K too large");
 
   const int vec = 16 / esz;
-  const int bk = esz == 4 ? 32 : 64;
+  const int bk = 128 / esz;  // K tile: 128 bytes per row
   int la = operand_layout(d, a, 0, vec, bk);
   int lb = operand_layout(d, b, 1, vec, bk);
   if (nk == 0) la = lb = kGeneric;  // nothing to load: the generic kernel writes zeros
@@ -99,6 +99,11 @@ extern "C" int es_contract(const es_contract_desc* d, const void* a, const void*
   p.batch = uint32_t(nb);
   p.ka_inner = d->n_k > 0 ? d->k[d->n_k - 1].a : 0;
   p.kb_inner = d->n_k > 0 ? d->k[d->n_k - 1].b : 0;
+  p.k_inner = d->n_k > 0 ? uint32_t(d->k[d->n_k - 1].size) : 0;
+  // the fast kernels walk K incrementally over at most two sub-axes
+  if (d->n_k > 2) la = lb = kGeneric;
+  p.ka_outer = d->n_k == 2 ? d->k[0].a : int64_t(p.k_inner) * p.ka_inner;
+  p.kb_outer = d->n_k == 2 ? d->k[0].b : int64_t(p.k_inner) * p.kb_inner;
   p.vstore = 0;
   if (d->n_n > 0) {
     const es_axis& nin = d->n[d->n_n - 1];

@@ -10,8 +10,9 @@ namespace contract {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
 
-// offset of linear index `i` of a group in the operand selected by `which`
+// offset of linear index `i` of a group in the operand selected by WHICH
 // (0 = A, 1 = B, 2 = C)
 template <int WHICH>
 __device__ __forceinline__ int64_t group_offset(const GroupArgs& g, uint32_t i) {
@@ -42,7 +43,6 @@ struct Traits<float> {
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(nfrag.z), __uint_as_float(mfrag.z), acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(nfrag.w), __uint_as_float(mfrag.w), acc, 0, 0, 0);
   }
-  static __device__ __forceinline__ float to_float(S v) { return v; }
   static __device__ __forceinline__ S from_float(float v) { return v; }
 };
 
@@ -54,7 +54,6 @@ struct Traits<bf16_t> {
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, nfrag), __builtin_bit_cast(bf16x8, mfrag),
                                                   acc, 0, 0, 0);
   }
-  static __device__ __forceinline__ float to_float(S v) { return bf16_to_f32(v); }
   static __device__ __forceinline__ S from_float(float v) { return f32_to_bf16(v); }
 };
 
@@ -66,25 +65,33 @@ struct Traits<f16_t> {
     acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, nfrag), __builtin_bit_cast(f16x8, mfrag),
                                                  acc, 0, 0, 0);
   }
-  static __device__ __forceinline__ float to_float(S v) { return Elem<f16_t>::load(v); }
   static __device__ __forceinline__ S from_float(float v) { return Elem<f16_t>::store(v); }
 };
+
+// ---- LDS tile geometry -----------------------------------------------------------
+// A tile is ROWS rows of BK elements (128 bytes for every element type: BK = 64 for
+// 16-bit types, 32 for fp32), K-contiguous, no padding.  The 16-byte chunk c of row r
+// lives at chunk position c ^ ((r / 2) % 8): sixteen consecutive rows then cover all
+// sixteen 16-byte slots of a 256-byte LDS line, so the fragment reads (32 consecutive
+// rows, one chunk) and the global->LDS writes are free of bank conflicts.
+constexpr int kRowBytes = 128;
+constexpr int kChunks = kRowBytes / 16;  // 8
+
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & (kChunks - 1)); }
 
 // ---- register transposes for MN-contiguous tiles -----------------------------
 // in[r] holds VEC consecutive mn-elements of k-row r; out[j] holds the VEC
 // k-elements of mn-column j.
 __device__ __forceinline__ void transpose_block(const uint4 (&in)[8], uint4 (&out)[8]) {
-  // 16-bit elements, 8x8
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int p = j / 2;       // dword holding column j in each input row
-    const bool hi = j & 1;     // which half
+    const int p = j / 2;
+    const bool hi = j & 1;
     uint32_t w[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const uint32_t a = (&in[2 * q].x)[p];
       const uint32_t b = (&in[2 * q + 1].x)[p];
-      // low half <- a's selected half, high half <- b's selected half
       w[q] = hi ? __builtin_amdgcn_perm(b, a, 0x07060302u) : __builtin_amdgcn_perm(b, a, 0x05040100u);
     }
     out[j] = uint4{w[0], w[1], w[2], w[3]};
@@ -92,60 +99,81 @@ __device__ __forceinline__ void transpose_block(const uint4 (&in)[8], uint4 (&ou
 }
 
 __device__ __forceinline__ void transpose_block(const uint4 (&in)[4], uint4 (&out)[4]) {
-  // 32-bit elements, 4x4
 #pragma unroll
   for (int j = 0; j < 4; ++j) out[j] = uint4{(&in[0].x)[j], (&in[1].x)[j], (&in[2].x)[j], (&in[3].x)[j]};
 }
+
+// ---- incremental K walk ----------------------------------------------------------
+// Fast paths have at most two K sub-axes and the innermost one is a multiple of BK,
+// so the offset of K tile t+1 follows from tile t by additions only.
+struct KWalk {
+  uint32_t kin;    // position inside the innermost K sub-axis
+  int64_t off_a;   // element offset of the tile in A
+  int64_t off_b;   // ... in B
+  __device__ __forceinline__ void start() {
+    kin = 0;
+    off_a = 0;
+    off_b = 0;
+  }
+  __device__ __forceinline__ void advance(const ContractArgs& p, int bk) {
+    kin += bk;
+    off_a += int64_t(bk) * p.ka_inner;
+    off_b += int64_t(bk) * p.kb_inner;
+    if (kin == p.k_inner) {
+      kin = 0;
+      off_a += p.ka_outer - int64_t(p.k_inner) * p.ka_inner;
+      off_b += p.kb_outer - int64_t(p.k_inner) * p.kb_inner;
+    }
+  }
+};
 
 // ---- tile loaders -------------------------------------------------------------
 // SIDE 0 loads the M-side tile from A, SIDE 1 the N-side tile from B.
 template <typename T, int ROWS, int BK, int NT, int LAYOUT, int SIDE>
 struct Loader;
 
-// K-contiguous: 16-byte vectors along k
+// K-contiguous: direct global -> LDS copies (global_load_lds_dwordx4).  One wave
+// instruction fills one 1 KB region (8 rows x 128 bytes); lane l writes slot l, i.e.
+// row l / 8 and chunk position l % 8, so it fetches the logical chunk stored there.
 template <typename T, int ROWS, int BK, int NT, int SIDE>
 struct Loader<T, ROWS, BK, NT, kKContig, SIDE> {
   using S = typename Traits<T>::S;
   static constexpr int VEC = Traits<T>::VEC;
-  static constexpr int KV = BK / VEC;
-  static constexpr int RPP = NT / KV;  // rows per pass
-  static constexpr int NP = (ROWS + RPP - 1) / RPP;
-  static_assert(NT % KV == 0, "tile shape");
+  static constexpr int NW = NT / 64;
+  static constexpr int RPI = 64 / kChunks;  // rows per wave instruction
+  static constexpr int NI = ROWS / RPI / NW;
+  static_assert(NI >= 1 && ROWS % (RPI * NW) == 0, "tile shape");
+  static constexpr bool kDirect = true;
 
-  int64_t rowoff[NP];
-  uint4 reg[NP];
-  int kv, r0;
+  const S* src[NI];
+  int region0;  // first 1 KB region of this wave
 
   __device__ __forceinline__ void init(const ContractArgs& p, int tid, uint32_t row0, int64_t boff) {
-    kv = tid % KV;
-    r0 = tid / KV;
+    const int lane = tid % 64;
+    const int wave = tid / 64;
+    region0 = wave * NI;
     const GroupArgs& g = SIDE == 0 ? p.gm : p.gn;
     const uint32_t lim = (SIDE == 0 ? p.M : p.N) - 1;
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      uint32_t r = row0 + r0 + i * RPP;
-      r = r > lim ? lim : r;  // rows past the edge re-read the last row; never stored
-      rowoff[i] = boff + group_offset<SIDE>(g, r) + kv * VEC;
-    }
-  }
-
-  __device__ __forceinline__ void load(const ContractArgs& p, uint32_t k0) {
     const S* base = static_cast<const S*>(SIDE == 0 ? p.a : p.b);
-    const int64_t koff = group_offset<SIDE>(p.gk, k0);
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      if (ROWS % RPP == 0 || r0 + i * RPP < ROWS)
-        reg[i] = *reinterpret_cast<const uint4*>(base + rowoff[i] + koff);
+    for (int i = 0; i < NI; ++i) {
+      const int row = (region0 + i) * RPI + lane / kChunks;
+      const int chunk = swz(row, lane % kChunks);
+      uint32_t r = row0 + row;
+      r = r > lim ? lim : r;  // rows past the edge re-read the last row; never stored
+      src[i] = base + boff + group_offset<SIDE>(g, r) + chunk * VEC;
     }
   }
 
-  __device__ __forceinline__ void store(S* lds, int ldk) const {
+  // enqueue the copies of the K tile at element offset `koff` into LDS tile `dst`
+  __device__ __forceinline__ void issue(S* dst, int64_t koff) const {
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      if (ROWS % RPP == 0 || r0 + i * RPP < ROWS)
-        *reinterpret_cast<uint4*>(lds + (r0 + i * RPP) * ldk + kv * VEC) = reg[i];
-    }
+    for (int i = 0; i < NI; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(src[i] + koff), (lds_void*)(dst + (region0 + i) * 512 * 2 / sizeof(S)),
+                                       16, 0, 0);
   }
+  __device__ __forceinline__ void load(const ContractArgs&, uint32_t, int64_t) {}
+  __device__ __forceinline__ void store(S*) const {}
 };
 
 // MN-contiguous: VEC x VEC blocks loaded along mn, transposed in registers
@@ -156,8 +184,9 @@ struct Loader<T, ROWS, BK, NT, kMNContig, SIDE> {
   static constexpr int MG = ROWS / VEC;
   static constexpr int KG = BK / VEC;
   static constexpr int NB = (MG * KG + NT - 1) / NT;
+  static constexpr bool kDirect = false;
 
-  int64_t off[NB];
+  const S* src[NB];
   uint4 reg[NB][VEC];
   int mg[NB], kg[NB];
   int64_t kstride;
@@ -165,6 +194,7 @@ struct Loader<T, ROWS, BK, NT, kMNContig, SIDE> {
   __device__ __forceinline__ void init(const ContractArgs& p, int tid, uint32_t row0, int64_t boff) {
     const GroupArgs& g = SIDE == 0 ? p.gm : p.gn;
     const uint32_t lim = (SIDE == 0 ? p.M : p.N) - VEC;  // last full group (extent % VEC == 0)
+    const S* base = static_cast<const S*>(SIDE == 0 ? p.a : p.b);
     kstride = SIDE == 0 ? p.ka_inner : p.kb_inner;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
@@ -173,32 +203,32 @@ struct Loader<T, ROWS, BK, NT, kMNContig, SIDE> {
       kg[j] = b / MG;
       uint32_t r = row0 + mg[j] * VEC;
       r = r > lim ? lim : r;
-      off[j] = boff + group_offset<SIDE>(g, r) + int64_t(kg[j] * VEC) * kstride;
+      src[j] = base + boff + group_offset<SIDE>(g, r) + int64_t(kg[j] * VEC) * kstride;
     }
   }
+  __device__ __forceinline__ void issue(S*, int64_t) const {}
 
-  __device__ __forceinline__ void load(const ContractArgs& p, uint32_t k0) {
-    const S* base = static_cast<const S*>(SIDE == 0 ? p.a : p.b);
-    const int64_t koff = group_offset<SIDE>(p.gk, k0);
+  __device__ __forceinline__ void load(const ContractArgs&, uint32_t, int64_t koff) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       if ((MG * KG) % NT == 0 || kg[j] < KG) {
 #pragma unroll
-        for (int kk = 0; kk < VEC; ++kk)
-          reg[j][kk] = *reinterpret_cast<const uint4*>(base + off[j] + koff + kk * kstride);
+        for (int kk = 0; kk < VEC; ++kk) reg[j][kk] = *reinterpret_cast<const uint4*>(src[j] + koff + kk * kstride);
       }
     }
   }
 
-  __device__ __forceinline__ void store(S* lds, int ldk) const {
+  __device__ __forceinline__ void store(S* lds) const {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       if ((MG * KG) % NT == 0 || kg[j] < KG) {
         uint4 t[VEC];
         transpose_block(reg[j], t);
 #pragma unroll
-        for (int jj = 0; jj < VEC; ++jj)
-          *reinterpret_cast<uint4*>(lds + (mg[j] * VEC + jj) * ldk + kg[j] * VEC) = t[jj];
+        for (int jj = 0; jj < VEC; ++jj) {
+          const int row = mg[j] * VEC + jj;
+          *reinterpret_cast<uint4*>(lds + row * BK + swz(row, kg[j]) * VEC) = t[jj];
+        }
       }
     }
   }
@@ -208,9 +238,11 @@ struct Loader<T, ROWS, BK, NT, kMNContig, SIDE> {
 template <typename T, int ROWS, int BK, int NT, int SIDE>
 struct Loader<T, ROWS, BK, NT, kGeneric, SIDE> {
   using S = typename Traits<T>::S;
+  static constexpr int VEC = Traits<T>::VEC;
   static constexpr int RPP = NT / BK;
   static constexpr int NE = (ROWS + RPP - 1) / RPP;
   static_assert(NT % BK == 0, "tile shape");
+  static constexpr bool kDirect = false;
 
   int64_t rowoff[NE];
   bool rowok[NE];
@@ -229,8 +261,9 @@ struct Loader<T, ROWS, BK, NT, kGeneric, SIDE> {
       rowoff[i] = rowok[i] ? boff + group_offset<SIDE>(g, r) : 0;
     }
   }
+  __device__ __forceinline__ void issue(S*, int64_t) const {}
 
-  __device__ __forceinline__ void load(const ContractArgs& p, uint32_t k0) {
+  __device__ __forceinline__ void load(const ContractArgs& p, uint32_t k0, int64_t) {
     const S* base = static_cast<const S*>(SIDE == 0 ? p.a : p.b);
     const uint32_t k = k0 + kk;
     const bool kok = k < p.K;
@@ -239,28 +272,94 @@ struct Loader<T, ROWS, BK, NT, kGeneric, SIDE> {
     for (int i = 0; i < NE; ++i) reg[i] = (kok && rowok[i]) ? base[rowoff[i] + koff] : S(0);
   }
 
-  __device__ __forceinline__ void store(S* lds, int ldk) const {
+  __device__ __forceinline__ void store(S* lds) const {
 #pragma unroll
-    for (int i = 0; i < NE; ++i)
-      if (r0 + i * RPP < ROWS) lds[(r0 + i * RPP) * ldk + kk] = reg[i];
+    for (int i = 0; i < NE; ++i) {
+      const int row = r0 + i * RPP;
+      if (row < ROWS) lds[row * BK + swz(row, kk / VEC) * VEC + kk % VEC] = reg[i];
+    }
   }
 };
 
+// ---- epilogue write-out ----------------------------------------------------------
+// Staged row r (of SROWS = WM * 32) is output row mbase + (r / 32) * WTM + r % 32.
+// The output group descriptors are read through a volatile pointer into the kernel
+// argument segment (the ContractArgs parameter sits at its start), so they are loaded
+// here, where they are used, instead of being held in scalar registers through the
+// whole K loop.
+template <int WHICH>
+__device__ __forceinline__ int64_t group_offset_v(const volatile GroupArgs& g, uint32_t i) {
+  int64_t off = 0;
+  const int n = g.n;
+  for (int d = n - 1; d >= 0; --d) {
+    FastDiv f;
+    f.d = g.div[d].d;
+    f.m = g.div[d].m;
+    f.l = g.div[d].l;
+    uint32_t r;
+    i = f.divmod(i, r);
+    off += int64_t(r) * (WHICH == 0 ? g.sa[d] : (WHICH == 1 ? g.sb[d] : g.sc[d]));
+  }
+  return off;
+}
+
+template <typename S, int BN, int WM, int NT>
+__device__ __forceinline__ void write_out(const ContractArgs& p, const S* stage, uint32_t mbase, int wtm, uint32_t n0,
+                                       int64_t boff_c, int tid) {
+  constexpr int VEC = 16 / int(sizeof(S));
+  constexpr int SROWS = WM * 32;
+  constexpr int SLD = BN + VEC;
+  S* C = static_cast<S*>(p.c);
+#if defined(__HIP_DEVICE_COMPILE__)
+  const volatile ContractArgs* kp =
+      reinterpret_cast<const volatile ContractArgs*>(__builtin_amdgcn_kernarg_segment_ptr());
+#else
+  const volatile ContractArgs* kp = &p;  // host pass: parsed, never executed
+#endif
+  if (p.vstore) {
+    constexpr int CV = BN / VEC;  // vectors per staged row
+    for (int v = tid; v < SROWS * CV; v += NT) {
+      const int r = v / CV;
+      const int cv = v - r * CV;
+      const uint32_t m = mbase + (r / 32) * wtm + r % 32;
+      const uint32_t n = n0 + cv * VEC;
+      if (m < p.M && n < p.N) {
+        const int64_t off = boff_c + group_offset_v<2>(kp->gm, m) + group_offset_v<2>(kp->gn, n);
+        *reinterpret_cast<uint4*>(C + off) = *reinterpret_cast<const uint4*>(stage + r * SLD + cv * VEC);
+      }
+    }
+  } else {
+    for (int v = tid; v < SROWS * BN; v += NT) {
+      const int r = v / BN;
+      const int cn = v - r * BN;
+      const uint32_t m = mbase + (r / 32) * wtm + r % 32;
+      const uint32_t n = n0 + cn;
+      if (m < p.M && n < p.N) C[boff_c + group_offset_v<2>(kp->gm, m) + group_offset_v<2>(kp->gn, n)] = stage[r * SLD + cn];
+    }
+  }
+}
+
 // ---- the kernel ----------------------------------------------------------------
-template <typename T, int BM, int BN, int BK, int WM, int WN, int LA, int LB>
+// PF > 1: K-contiguous operands also pull K tile kt + PF into L2 (a 4-byte LDS-DMA
+// per 128-byte row into a scratch slot), so the copies of tile kt + 1 find it there.
+template <typename T, int BM, int BN, int WM, int WN, int LA, int LB, int PF>
 __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const ContractArgs p) {
   using S = typename Traits<T>::S;
   constexpr int NT = WM * WN * 64;
   constexpr int VEC = Traits<T>::VEC;
-  constexpr int LDK = BK + VEC;  // LDS row pitch (elements): +16 bytes
-  constexpr int KSTEP = 2 * VEC; // k consumed per fragment read
+  constexpr int BK = kRowBytes / int(sizeof(S));
+  constexpr int KSTEP = 2 * VEC;  // k consumed per fragment read
+  constexpr int NS = BK / KSTEP;  // fragment steps per K tile
   constexpr int WTM = BM / WM;
   constexpr int WTN = BN / WN;
   constexpr int FM = WTM / 32;
   constexpr int FN = WTN / 32;
-  static_assert(FM >= 1 && FN >= 1 && BK % KSTEP == 0, "tile shape");
+  constexpr int STAGE = (BM + BN) * BK;  // elements per LDS stage
+  constexpr bool kGen = LA == kGeneric || LB == kGeneric;
+  static_assert(FM >= 1 && FN >= 1, "tile shape");
 
-  __shared__ __attribute__((aligned(16))) S lds[2][(BM + BN) * LDK];
+  __shared__ __attribute__((aligned(1024))) S lds[2 * STAGE];
+  __shared__ __attribute__((aligned(256))) uint32_t sink[64];
 
   const int tid = threadIdx.x;
   const int lane = tid % 64;
@@ -290,6 +389,36 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const Contrac
   la.init(p, tid, m0, boff_a);
   lb.init(p, tid, n0, boff_b);
 
+  // L2 touch addresses: one per 128-byte row of the K-contiguous tiles
+  constexpr bool kTouch = PF > 1 && (LA == kKContig || LB == kKContig);
+  constexpr int kTouchRows = (LA == kKContig ? BM : 0) + (LB == kKContig ? BN : 0);
+  constexpr int kTouches = kTouch ? (kTouchRows + NT - 1) / NT : 0;
+  const S* touch_src[kTouches > 0 ? kTouches : 1];
+  if constexpr (kTouch) {
+#pragma unroll
+    for (int q = 0; q < kTouches; ++q) {
+      int row = tid + q * NT;
+      if (row >= kTouchRows) row = kTouchRows - 1;
+      const bool on_a = LA == kKContig && row < BM;
+      const int r = LA == kKContig ? (on_a ? row : row - BM) : row;
+      const uint32_t lim = (on_a ? p.M : p.N) - 1;
+      const uint32_t g = min((on_a ? m0 : n0) + r, lim);
+      touch_src[q] = static_cast<const S*>(on_a ? p.a : p.b) + (on_a ? boff_a : boff_b) +
+                     (on_a ? group_offset<0>(p.gm, g) : group_offset<1>(p.gn, g));
+    }
+  }
+  auto touch = [&](int64_t koff_a, int64_t koff_b) {
+    if constexpr (kTouch) {
+#pragma unroll
+      for (int q = 0; q < kTouches; ++q) {
+        const int row = tid + q * NT;
+        const bool on_a = LA == kKContig && row < BM;
+        __builtin_amdgcn_global_load_lds((const void*)(touch_src[q] + (on_a ? koff_a : koff_b)), (lds_void*)sink, 4, 0,
+                                         0);
+      }
+    }
+  };
+
   f32x16 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -299,44 +428,92 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const Contrac
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const uint32_t nk = (p.K + BK - 1) / BK;
+  KWalk kw;  // offset of the next tile to fetch
+  kw.start();
+  KWalk tw;  // offset of the next tile to touch
+  tw.start();
   if (nk > 0) {
-    la.load(p, 0);
-    lb.load(p, 0);
-    la.store(&lds[0][0], LDK);
-    lb.store(&lds[0][BM * LDK], LDK);
+    la.issue(&lds[0], kw.off_a);
+    lb.issue(&lds[BM * BK], kw.off_b);
+    la.load(p, 0, kw.off_a);
+    lb.load(p, 0, kw.off_b);
+    la.store(&lds[0]);
+    lb.store(&lds[BM * BK]);
+    if (!kGen) kw.advance(p, BK);
+    if constexpr (kTouch) {
+      tw.advance(p, BK);
+#pragma unroll
+      for (int d = 1; d < PF; ++d) {
+        if (uint32_t(d) < nk) touch(tw.off_a, tw.off_b);
+        if (uint32_t(d) < nk) tw.advance(p, BK);
+      }
+    }
   }
-  __syncthreads();
+
+  // fragment rows of this lane
+  int arow[FM], brow[FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) arow[i] = wm * WTM + i * 32 + lane % 32;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) brow[j] = wn * WTN + j * 32 + lane % 32;
 
   for (uint32_t kt = 0; kt < nk; ++kt) {
+    // Tile kt's copies must have landed.  Vector-memory loads complete in issue
+    // order; the only loads issued after them are the touches of the previous
+    // iteration (its staged register loads were consumed by its LDS stores), so
+    // leaving exactly that many outstanding is enough.
+    if (kTouch && kt >= 1 && kt - 1 + PF < nk) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kTouches) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
     const int cur = kt & 1;
     const bool more = kt + 1 < nk;
     if (more) {
-      la.load(p, (kt + 1) * BK);
-      lb.load(p, (kt + 1) * BK);
+      S* nxt = &lds[(cur ^ 1) * STAGE];
+      la.issue(nxt, kw.off_a);
+      lb.issue(nxt + BM * BK, kw.off_b);
+      la.load(p, (kt + 1) * BK, kw.off_a);
+      lb.load(p, (kt + 1) * BK, kw.off_b);
+      if (!kGen) kw.advance(p, BK);
+      if constexpr (kTouch) {
+        if (kt + PF < nk) {
+          touch(tw.off_a, tw.off_b);
+          tw.advance(p, BK);
+        }
+      }
     }
-    const S* As = &lds[cur][0];
-    const S* Bs = &lds[cur][BM * LDK];
-#pragma unroll
-    for (int ks = 0; ks < BK / KSTEP; ++ks) {
-      const int kofs = ks * KSTEP + (lane / 32) * VEC;
-      uint4 af[FM], bf[FN];
+    const S* As = &lds[cur * STAGE];
+    const S* Bs = As + BM * BK;
+    uint4 af[2][FM], bf[2][FN];
+    auto frags = [&](int buf, int ks) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        af[i] = *reinterpret_cast<const uint4*>(As + (wm * WTM + i * 32 + lane % 32) * LDK + kofs);
+        af[buf][i] = *reinterpret_cast<const uint4*>(As + arow[i] * BK + swz(arow[i], ks * 2 + lane / 32) * VEC);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bf[j] = *reinterpret_cast<const uint4*>(Bs + (wn * WTN + j * 32 + lane % 32) * LDK + kofs);
+        bf[buf][j] = *reinterpret_cast<const uint4*>(Bs + brow[j] * BK + swz(brow[j], ks * 2 + lane / 32) * VEC);
+    };
+    frags(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < NS; ++ks) {
+      if (ks + 1 < NS) frags((ks + 1) & 1, ks + 1);
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) Traits<T>::mma(acc[i][j], bf[j], af[i]);
+        for (int j = 0; j < FN; ++j) Traits<T>::mma(acc[i][j], bf[ks & 1][j], af[ks & 1][i]);
+      __builtin_amdgcn_s_setprio(0);
     }
     if (more) {
-      la.store(&lds[cur ^ 1][0], LDK);
-      lb.store(&lds[cur ^ 1][BM * LDK], LDK);
+      S* nxt = &lds[(cur ^ 1) * STAGE];
+      la.store(nxt);
+      lb.store(nxt + BM * BK);
     }
-    __syncthreads();
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
 
   // ---- epilogue --------------------------------------------------------------
   // acc[i][j] holds C^T of a 32x32 block.  Pass i stages rows
@@ -346,9 +523,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const Contrac
   // stores otherwise.
   constexpr int SROWS = WM * 32;
   constexpr int SLD = BN + VEC;  // staging row pitch (elements)
-  static_assert(SROWS * SLD <= 2 * (BM + BN) * LDK, "staging tile must fit in LDS");
-  S* stage = &lds[0][0];
-  S* C = static_cast<S*>(p.c);
+  static_assert(SROWS * SLD <= 2 * STAGE, "staging tile must fit in LDS");
+  S* stage = &lds[0];
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int srow = wm * 32 + lane % 32;
@@ -371,59 +547,36 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const Contrac
       }
     }
     __syncthreads();
-    // staged row r is output row m0 + (r / 32) * WTM + i * 32 + r % 32
-    if (p.vstore) {
-      constexpr int CV = BN / VEC;  // vectors per staged row
-      for (int v = tid; v < SROWS * CV; v += NT) {
-        const int r = v / CV;
-        const int cv = v - r * CV;
-        const uint32_t m = m0 + (r / 32) * WTM + i * 32 + r % 32;
-        const uint32_t n = n0 + cv * VEC;
-        if (m < p.M && n < p.N) {
-          const int64_t off = boff_c + group_offset<2>(p.gm, m) + group_offset<2>(p.gn, n);
-          *reinterpret_cast<uint4*>(C + off) = *reinterpret_cast<const uint4*>(stage + r * SLD + cv * VEC);
-        }
-      }
-    } else {
-      for (int v = tid; v < SROWS * BN; v += NT) {
-        const int r = v / BN;
-        const int cn = v - r * BN;
-        const uint32_t m = m0 + (r / 32) * WTM + i * 32 + r % 32;
-        const uint32_t n = n0 + cn;
-        if (m < p.M && n < p.N)
-          C[boff_c + group_offset<2>(p.gm, m) + group_offset<2>(p.gn, n)] = stage[r * SLD + cn];
-      }
-    }
+    write_out<S, BN, WM, NT>(p, stage, m0 + i * 32, WTM, n0, boff_c, tid);
     __syncthreads();
   }
 }
 
 // ---- launcher ----------------------------------------------------------------------
-template <typename T, int BM, int BN, int BK, int WM, int WN, int LA, int LB>
+template <typename T, int BM, int BN, int WM, int WN, int LA, int LB, int PF>
 int launch_one(const ContractArgs& p, hipStream_t s, const char* name) {
-  contract_kernel<T, BM, BN, BK, WM, WN, LA, LB><<<p.total_tiles, WM * WN * 64, 0, s>>>(p);
+  contract_kernel<T, BM, BN, WM, WN, LA, LB, PF><<<p.total_tiles, WM * WN * 64, 0, s>>>(p);
   set_kernel(name);
   return check_launch("es_contract");
 }
 
-template <typename T, int BM, int BN, int BK, int WM, int WN>
+template <typename T, int BM, int BN, int WM, int WN, int PF>
 int launch_layouts(const ContractArgs& p, int la, int lb, hipStream_t s, const char* name) {
-  if (la == kKContig && lb == kKContig) return launch_one<T, BM, BN, BK, WM, WN, kKContig, kKContig>(p, s, name);
-  if (la == kKContig && lb == kMNContig) return launch_one<T, BM, BN, BK, WM, WN, kKContig, kMNContig>(p, s, name);
-  if (la == kMNContig && lb == kKContig) return launch_one<T, BM, BN, BK, WM, WN, kMNContig, kKContig>(p, s, name);
-  if (la == kMNContig && lb == kMNContig) return launch_one<T, BM, BN, BK, WM, WN, kMNContig, kMNContig>(p, s, name);
+  if (la == kKContig && lb == kKContig) return launch_one<T, BM, BN, WM, WN, kKContig, kKContig, PF>(p, s, name);
+  if (la == kKContig && lb == kMNContig) return launch_one<T, BM, BN, WM, WN, kKContig, kMNContig, PF>(p, s, name);
+  if (la == kMNContig && lb == kKContig) return launch_one<T, BM, BN, WM, WN, kMNContig, kKContig, PF>(p, s, name);
+  if (la == kMNContig && lb == kMNContig) return launch_one<T, BM, BN, WM, WN, kMNContig, kMNContig, 1>(p, s, name);
   return fail(ES_ERR_INVALID, "es_contract: layout combination has no fast kernel");
 }
 
 template <typename T>
 int launch_typed(const ContractArgs& p, int config, int la, int lb, hipStream_t s) {
-  constexpr int BK = sizeof(typename Traits<T>::S) == 4 ? 32 : 64;
   if (la == kGeneric || lb == kGeneric)
-    return launch_one<T, 64, 64, 32, 2, 2, kGeneric, kGeneric>(p, s, "contract_generic_64x64");
+    return launch_one<T, 64, 64, 2, 2, kGeneric, kGeneric, 1>(p, s, "contract_generic_64x64");
   switch (config) {
-    case 0: return launch_layouts<T, 256, 256, BK, 2, 2>(p, la, lb, s, "contract_256x256");
-    case 1: return launch_layouts<T, 128, 128, BK, 2, 2>(p, la, lb, s, "contract_128x128");
-    default: return launch_layouts<T, 64, 64, BK, 2, 2>(p, la, lb, s, "contract_64x64");
+    case 0: return launch_layouts<T, 256, 256, 2, 4, 1>(p, la, lb, s, "contract_256x256");
+    case 1: return launch_layouts<T, 128, 128, 2, 2, 1>(p, la, lb, s, "contract_128x128");
+    default: return launch_layouts<T, 64, 64, 2, 2, 1>(p, la, lb, s, "contract_64x64");
   }
 }
 
