@@ -10,12 +10,14 @@ the configuration the north star's headline target (>= 70 % of bf16 MFMA peak)
 is quoted on.  The other configs are parity cases; ``--workload`` measures them
 individually with the same method.
 
-Timing: W untimed warm-up steps, then K steps between two device
-synchronisations (wall clock -> ms_per_step) with HIP events recorded on the
-stream the kernel runs on (torch's current stream, which the library launches
-on) -> the kernel's average duration.  HBM-bound workloads write a 512 MiB
-buffer between steps so their inputs are not served from the 256 MB Infinity
-Cache; those steps are timed one by one with events (the flush is not timed).
+Timing: W untimed warm-up steps, then K back-to-back steps between two device
+synchronisations (wall clock -> ms_per_step, value: host work included).  The
+kernel's average duration (roofline.achieved) comes from HIP events recorded on
+the stream the kernel runs on (torch's current stream, which the library
+launches on) around K more launches queued behind a bounded spin kernel, so
+they run back to back without host gaps.  For HBM-bound workloads K more
+launches follow, each after a 512 MiB fill that evicts the 256 MB Infinity
+Cache (fill not timed): roofline.kernel_ms_cold.
 
 roofline.achieved uses algorithmic work only: 2*M*N*K flops for contractions,
 unique input bytes + output bytes for the copy / reduce / broadcast kernels.
@@ -36,6 +38,10 @@ for _path in (os.path.join(_REPO, "torch-einshard_amd"), _REPO):
         sys.path.insert(0, _path)
 
 import torch  # noqa: E402
+
+# spin of the queue-priming kernel: ~10-25 ms, far longer than the host needs
+# to enqueue K launches
+PRIME_CYCLES = 50_000_000
 
 METRIC = "einshard contraction TFLOP/s; einwindow/reduce GB/s; % of MI355X roofline"
 PEAK = {
@@ -224,39 +230,46 @@ def _cpu_runner(wl):
 def measure_gpu(es, wl, dev, steps, warmup):
     xs = [t.to(dev) for t in wl["host"]]
     run = _runner(es, wl)
-    flush = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev) if wl["bound"] == "hbm" else None
     for _ in range(warmup):
         run(xs)
-    torch.cuda.synchronize(dev)
     stream = torch.cuda.current_stream(dev)
-    if flush is None:
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize(dev)
-        t0 = time.perf_counter()
-        start.record(stream)
-        for _ in range(steps):
-            out = run(xs)
-        end.record(stream)
-        torch.cuda.synchronize(dev)
-        wall = time.perf_counter() - t0
-        kernel_ms = start.elapsed_time(end) / steps
-    else:
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = run(xs)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    del out
+    # kernel time: the same K launches behind a bounded spin kernel, so that the
+    # host has enqueued all of them before the first starts and the two events
+    # bracket back-to-back kernels only (no host gaps)
+    torch.cuda._sleep(PRIME_CYCLES)
+    start.record(stream)
+    for _ in range(steps):
+        out = run(xs)
+    end.record(stream)
+    torch.cuda.synchronize(dev)
+    kernel_ms = start.elapsed_time(end) / steps
+    del out
+    cold_ms = None
+    if wl["bound"] == "hbm":
+        # the same launches with the 256 MB Infinity Cache flushed before each
+        # one (a 512 MiB fill, not timed): shows whether back-to-back steps were
+        # served from cache
+        flush = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev)
         events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-        torch.cuda.synchronize(dev)
-        t0 = time.perf_counter()
         for s, e in events:
             flush.fill_(1)
             s.record(stream)
             out = run(xs)
             e.record(stream)
         torch.cuda.synchronize(dev)
-        wall = time.perf_counter() - t0
-        kernel_ms = sum(s.elapsed_time(e) for s, e in events) / steps
+        cold_ms = sum(s.elapsed_time(e) for s, e in events) / steps
+        del out, flush
     from torch_einshard import _native
 
-    kernel_name = _native.last_kernel()
-    del out
-    return dict(wall_s=wall, kernel_ms=kernel_ms, kernel=kernel_name)
+    return dict(wall_s=wall, kernel_ms=kernel_ms, cold_ms=cold_ms, kernel=_native.last_kernel())
 
 
 def measure_cpu(wl, budget_s=12.0):
@@ -313,6 +326,8 @@ def bench_one(es, key, dev, steps, warmup, cpu=True):
         kernel=g["kernel"],
         kernel_ms=round(g["kernel_ms"], 5),
     )
+    if g["cold_ms"] is not None:
+        roofline["kernel_ms_cold"] = round(g["cold_ms"], 5)
     line = {
         "metric": METRIC,
         "value": round(value, 3),

@@ -267,3 +267,25 @@ def test_unsupported_dtype_for_arithmetic(gpu):
 def test_cpu_tensors_are_refused(gpu):
     with pytest.raises(RuntimeError, match="device tensors"):
         es.einshard("a b -> b a", torch.ones(2, 3))
+
+
+# ---- prepared-launch replay -----------------------------------------------------------
+
+
+def test_repeated_calls_replay_with_fresh_data_and_geometry(gpu):
+    expr = "a b k c, b c l d -> k l d a"
+    for seed in (40, 41):  # the second call replays the first call's prepared launch
+        x, y = randn(4, 5, 8, 6, seed=seed), randn(5, 6, 8, 3, seed=seed + 100)
+        assert_rel(es.einshard(expr, x.to(gpu), y.to(gpu)), einshard_cpu(expr, x, y), TOL[torch.float32])
+        assert [step.name for step in last_plan()] == ["rank_local_einsum"]
+    # same shapes, other strides: a new plan, not the cached one
+    xt = randn(4, 5, 6, 8, seed=42).to(gpu).transpose(2, 3)
+    y = randn(5, 6, 8, 3, seed=43)
+    assert_rel(es.einshard(expr, xt, y.to(gpu)), einshard_cpu(expr, xt.cpu(), y), TOL[torch.float32])
+    # same geometry on the host after a cached device call: still refused
+    with pytest.raises(RuntimeError, match="device tensors"):
+        es.einshard(expr, xt.cpu(), y)
+    # a factored output packs on replay too
+    x = randn(6, 4, seed=44)
+    for _ in range(2):
+        assert_bitexact(es.einshard("h p -> (p h)", x.to(gpu)), x.t().reshape(-1))

@@ -14,7 +14,7 @@ from . import _native
 from ._native import MAX_AXES, BcastDesc, ContractDesc, GatherDesc, ReduceDesc, call
 from .planner import BcastOp, ContractOp, EmptyOp, GatherOp, ReduceOp
 
-__all__ = ["check_device_tensors", "run_op", "run_gather", "dtype_code", "fill_bits"]
+__all__ = ["check_device_tensors", "run_op", "run_gather", "dtype_code", "fill_bits", "Prepared", "prepare_op", "launch"]
 
 _ELEM_SIZES = {1, 2, 4, 8}
 
@@ -64,6 +64,47 @@ def _set_axes(array, axes, what):
     return len(axes)
 
 
+class Prepared:
+    """One planned launch.  The descriptor is built (and the reduction workspace
+    size queried) once; a call then only allocates the output and binds data
+    pointers, so a repeated expression costs one ctypes call on the host."""
+
+    __slots__ = ("entry", "desc", "ref", "out_shape", "order", "workspace", "noop")
+
+    def __init__(self, entry, desc, out_shape, order, workspace=0, noop=False):
+        self.entry = entry
+        self.desc = desc
+        self.ref = ctypes.byref(desc) if desc is not None else None
+        self.out_shape = tuple(out_shape)
+        self.order = order
+        self.workspace = workspace
+        self.noop = noop
+
+
+def _raw_stream(device):
+    return torch._C._cuda_getCurrentRawStream(device.index if device.index is not None else torch.cuda.current_device())
+
+
+def launch(prep, xs, device, dtype):
+    """Allocate the output and enqueue ``prep`` on the current stream of ``device``."""
+    out = torch.empty(prep.out_shape, dtype=dtype, device=device)
+    if prep.noop or out.numel() == 0:
+        return out
+    handle = _native.lib()
+    fn = getattr(handle, prep.entry)
+    stream = _raw_stream(device)
+    ptrs = [xs[i].data_ptr() for i in prep.order]
+    if prep.entry == "es_reduce":
+        need = prep.workspace
+        ws = torch.empty(need, dtype=torch.uint8, device=device) if need > 0 else None
+        status = fn(prep.ref, ptrs[0], ptrs[1], out.data_ptr(), ws.data_ptr() if ws is not None else None, need, stream)
+    else:
+        status = fn(prep.ref, *ptrs, out.data_ptr(), stream)
+    if status < 0:
+        raise _native.NativeError(prep.entry, status, handle.es_last_error().decode())
+    return out
+
+
 def _ptr(tensor):
     return ctypes.c_void_p(tensor.data_ptr())
 
@@ -72,19 +113,17 @@ def run_gather(desc, x, out):
     call("es_gather", ctypes.byref(desc), _ptr(x), _ptr(out), _native.stream_of(out))
 
 
-def run_op(op, xs, dtype, device):
-    """Execute a planner op over operands ``xs`` (one or two tensors)."""
-    out = torch.empty(op.out_shape, dtype=dtype, device=device)
-    if isinstance(op, EmptyOp) or out.numel() == 0:
-        return out
-    stream = _native.stream_of(out)
+def prepare_op(op, dtype, elem_size):
+    """Build the descriptor of a planner op for operands of ``dtype``."""
+    if isinstance(op, EmptyOp) or any(size == 0 for size in op.out_shape):
+        # nothing to compute: an empty output of any dtype, like torch.einsum
+        return Prepared(None, None, op.out_shape, (), noop=True)
 
     if isinstance(op, GatherOp):
         desc = GatherDesc()
-        elem = xs[0].element_size()
-        if elem not in _ELEM_SIZES:
-            raise NotImplementedError(f"einshard: element size {elem} is not supported")
-        desc.elem_size = elem
+        if elem_size not in _ELEM_SIZES:
+            raise NotImplementedError(f"einshard: element size {elem_size} is not supported")
+        desc.elem_size = elem_size
         desc.boundary = 0
         desc.fill_bits = 0
         axes = op.axes or []
@@ -104,8 +143,7 @@ def run_op(op, xs, dtype, device):
                 desc.offset[i] = 0
                 desc.pos[i] = i
                 desc.win[i] = -1
-        call("es_gather", ctypes.byref(desc), _ptr(xs[0]), _ptr(out), stream)
-        return out
+        return Prepared("es_gather", desc, op.out_shape, (0,))
 
     code = dtype_code(dtype, "einshard")
 
@@ -113,8 +151,7 @@ def run_op(op, xs, dtype, device):
         desc = BcastDesc()
         desc.dtype = code
         desc.rank = _set_axes(desc.axes, op.axes, "einshard")
-        call("es_bcast", ctypes.byref(desc), _ptr(xs[0]), _ptr(xs[1]), _ptr(out), stream)
-        return out
+        return Prepared("es_bcast", desc, op.out_shape, (0, 1))
 
     if isinstance(op, ReduceOp):
         desc = ReduceDesc()
@@ -122,20 +159,8 @@ def run_op(op, xs, dtype, device):
         desc.has_y = 1 if op.has_y else 0
         desc.n_keep = _set_axes(desc.keep, op.keep, "einshard")
         desc.n_red = _set_axes(desc.red, op.red, "einshard")
-        need = call("es_reduce_workspace_bytes", ctypes.byref(desc))
-        workspace = torch.empty(max(int(need), 1), dtype=torch.uint8, device=device) if need > 0 else None
-        y = xs[1] if op.has_y else xs[0]
-        call(
-            "es_reduce",
-            ctypes.byref(desc),
-            _ptr(xs[0]),
-            _ptr(y),
-            _ptr(out),
-            _ptr(workspace) if workspace is not None else ctypes.c_void_p(0),
-            ctypes.c_int64(int(need) if need > 0 else 0),
-            stream,
-        )
-        return out
+        need = int(call("es_reduce_workspace_bytes", ctypes.byref(desc)))
+        return Prepared("es_reduce", desc, op.out_shape, (0, 1 if op.has_y else 0), workspace=need)
 
     if isinstance(op, ContractOp):
         desc = ContractDesc()
@@ -144,8 +169,11 @@ def run_op(op, xs, dtype, device):
         desc.n_m = _set_axes(desc.m, op.m, "einshard")
         desc.n_n = _set_axes(desc.n, op.n, "einshard")
         desc.n_k = _set_axes(desc.k, op.k, "einshard")
-        a, b = (xs[1], xs[0]) if op.swapped else (xs[0], xs[1])
-        call("es_contract", ctypes.byref(desc), _ptr(a), _ptr(b), _ptr(out), stream)
-        return out
+        return Prepared("es_contract", desc, op.out_shape, (1, 0) if op.swapped else (0, 1))
 
     raise TypeError(f"unknown planned op {type(op).__name__}")
+
+
+def run_op(op, xs, dtype, device):
+    """Execute a planner op over operands ``xs`` (one or two tensors)."""
+    return launch(prepare_op(op, dtype, xs[0].element_size()), xs, device, dtype)
