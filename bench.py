@@ -349,14 +349,22 @@ def bench_one(es, key, dev, steps, warmup, cpu=True):
 
 
 def _traffic(key):
-    """HBM bytes per launch measured with rocprofv3 counters (profiles/traffic.json), else None."""
-    path = os.path.join(_REPO, "profiles", "traffic.json")
+    """HBM bytes per launch of the workload's dominant kernel, measured with the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE counters (profiles/traffic.md), else None."""
+    path = os.path.join(_REPO, "profiles", "traffic.md")
     if not os.path.exists(path):
         return None
-    try:
-        return json.load(open(path)).get(key, {}).get("bytes_per_launch")
-    except (OSError, ValueError):
-        return None
+    header = None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if header is None and "bytes/launch" in cells:
+            header = cells
+        elif header is not None and len(cells) == len(header) and cells[0] == key:
+            try:
+                return int(cells[header.index("bytes/launch")])
+            except ValueError:
+                return None
+    return None
 
 
 def main(argv=None):
