@@ -281,12 +281,11 @@ struct Loader<T, ROWS, BK, NT, kGeneric, SIDE> {
   }
 };
 
-// ---- epilogue write-out ----------------------------------------------------------
-// Staged row r (of SROWS = WM * 32) is output row mbase + (r / 32) * WTM + r % 32.
+// ---- epilogue ------------------------------------------------------------------
 // The output group descriptors are read through a volatile pointer into the kernel
 // argument segment (the ContractArgs parameter sits at its start), so they are loaded
-// here, where they are used, instead of being held in scalar registers through the
-// whole K loop.
+// in the epilogue, where they are used, instead of being held in scalar registers
+// through the whole K loop.
 template <int WHICH>
 __device__ __forceinline__ int64_t group_offset_v(const volatile GroupArgs& g, uint32_t i) {
   int64_t off = 0;
@@ -303,12 +302,37 @@ __device__ __forceinline__ int64_t group_offset_v(const volatile GroupArgs& g, u
   return off;
 }
 
-template <typename S, int BN, int WM, int NT>
-__device__ __forceinline__ void write_out(const ContractArgs& p, const S* stage, uint32_t mbase, int wtm, uint32_t n0,
-                                       int64_t boff_c, int tid) {
+// LDS bytes the epilogue needs: the staged slice plus the row / column offset tables
+template <typename S, int BM, int BN, int WM>
+constexpr int epilogue_bytes() {
+  return WM * 32 * (BN + 16 / int(sizeof(S))) * int(sizeof(S)) + (BM + BN) * 8;
+}
+
+// acc[i][j] holds C^T of a 32x32 block.  The output offset of every tile row and
+// column is computed once (one thread each) into LDS tables; then pass i stages rows
+// {wm*WTM + i*32 + 0..31 : wm} (WM*32 rows x BN columns, converted to the element
+// type) in LDS as [row][n], and the whole work-group writes them out: 16-byte stores
+// along n when n is the output's contiguous axis, element stores otherwise.  `lds`
+// holds at least epilogue_bytes(); the caller has drained every copy into LDS and
+// synchronised the work-group.
+template <typename T, int BM, int BN, int WM, int WN, int FM, int FN>
+__device__ __forceinline__ void store_tile(const ContractArgs& p, void* lds, const f32x16 (&acc)[FM][FN], uint32_t m0,
+                                           uint32_t n0, int64_t boff_c) {
+  using S = typename Traits<T>::S;
+  constexpr int NT = WM * WN * 64;
   constexpr int VEC = 16 / int(sizeof(S));
+  constexpr int WTM = BM / WM;
+  constexpr int WTN = BN / WN;
   constexpr int SROWS = WM * 32;
-  constexpr int SLD = BN + VEC;
+  constexpr int SLD = BN + VEC;  // staging row pitch (elements)
+  S* stage = static_cast<S*>(lds);
+  int64_t* row_off = reinterpret_cast<int64_t*>(static_cast<char*>(lds) + SROWS * SLD * int(sizeof(S)));
+  int64_t* col_off = row_off + BM;
+  const int tid = threadIdx.x;
+  const int lane = tid % 64;
+  const int wave = tid / 64;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
   S* C = static_cast<S*>(p.c);
 #if defined(__HIP_DEVICE_COMPILE__)
   const volatile ContractArgs* kp =
@@ -316,26 +340,57 @@ __device__ __forceinline__ void write_out(const ContractArgs& p, const S* stage,
 #else
   const volatile ContractArgs* kp = &p;  // host pass: parsed, never executed
 #endif
-  if (p.vstore) {
-    constexpr int CV = BN / VEC;  // vectors per staged row
-    for (int v = tid; v < SROWS * CV; v += NT) {
-      const int r = v / CV;
-      const int cv = v - r * CV;
-      const uint32_t m = mbase + (r / 32) * wtm + r % 32;
-      const uint32_t n = n0 + cv * VEC;
-      if (m < p.M && n < p.N) {
-        const int64_t off = boff_c + group_offset_v<2>(kp->gm, m) + group_offset_v<2>(kp->gn, n);
-        *reinterpret_cast<uint4*>(C + off) = *reinterpret_cast<const uint4*>(stage + r * SLD + cv * VEC);
+  for (int r = tid; r < BM; r += NT) {
+    const uint32_t m = m0 + r;
+    row_off[r] = m < p.M ? boff_c + group_offset_v<2>(kp->gm, m) : -1;
+  }
+  for (int c = tid; c < BN; c += NT) {
+    const uint32_t n = n0 + c;
+    col_off[c] = n < p.N ? group_offset_v<2>(kp->gn, n) : -1;
+  }
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int srow = wm * 32 + lane % 32;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int scol = wn * WTN + j * 32 + 8 * g + 4 * (lane / 32);
+        S* dst = stage + srow * SLD + scol;
+        if constexpr (sizeof(S) == 4) {
+          *reinterpret_cast<float4*>(dst) =
+              float4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        } else {
+          const uint32_t lo = uint32_t(Traits<T>::from_float(acc[i][j][4 * g])) |
+                              (uint32_t(Traits<T>::from_float(acc[i][j][4 * g + 1])) << 16);
+          const uint32_t hi = uint32_t(Traits<T>::from_float(acc[i][j][4 * g + 2])) |
+                              (uint32_t(Traits<T>::from_float(acc[i][j][4 * g + 3])) << 16);
+          *reinterpret_cast<uint2*>(dst) = uint2{lo, hi};
+        }
       }
     }
-  } else {
-    for (int v = tid; v < SROWS * BN; v += NT) {
-      const int r = v / BN;
-      const int cn = v - r * BN;
-      const uint32_t m = mbase + (r / 32) * wtm + r % 32;
-      const uint32_t n = n0 + cn;
-      if (m < p.M && n < p.N) C[boff_c + group_offset_v<2>(kp->gm, m) + group_offset_v<2>(kp->gn, n)] = stage[r * SLD + cn];
+    __syncthreads();
+    // staged row r is tile row (r / 32) * WTM + i * 32 + r % 32
+    if (p.vstore) {
+      constexpr int CV = BN / VEC;  // vectors per staged row
+      for (int v = tid; v < SROWS * CV; v += NT) {
+        const int r = v / CV;
+        const int cv = v - r * CV;
+        const int64_t ro = row_off[(r / 32) * WTM + i * 32 + r % 32];
+        const int64_t co = col_off[cv * VEC];
+        if (ro >= 0 && co >= 0)
+          *reinterpret_cast<uint4*>(C + ro + co) = *reinterpret_cast<const uint4*>(stage + r * SLD + cv * VEC);
+      }
+    } else {
+      for (int v = tid; v < SROWS * BN; v += NT) {
+        const int r = v / BN;
+        const int cn = v - r * BN;
+        const int64_t ro = row_off[(r / 32) * WTM + i * 32 + r % 32];
+        const int64_t co = col_off[cn];
+        if (ro >= 0 && co >= 0) C[ro + co] = stage[r * SLD + cn];
+      }
     }
+    __syncthreads();
   }
 }
 
@@ -515,41 +570,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const Contrac
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
-  // ---- epilogue --------------------------------------------------------------
-  // acc[i][j] holds C^T of a 32x32 block.  Pass i stages rows
-  // {wm*WTM + i*32 + 0..31 : wm} (WM*32 rows x BN columns, converted to the
-  // element type) in LDS as [row][n], then the whole work-group writes them
-  // out: 16-byte stores along n when n is the output's contiguous axis, element
-  // stores otherwise.
-  constexpr int SROWS = WM * 32;
-  constexpr int SLD = BN + VEC;  // staging row pitch (elements)
-  static_assert(SROWS * SLD <= 2 * STAGE, "staging tile must fit in LDS");
-  S* stage = &lds[0];
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int srow = wm * 32 + lane % 32;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int scol = wn * WTN + j * 32 + 8 * g + 4 * (lane / 32);
-        S* dst = stage + srow * SLD + scol;
-        if constexpr (sizeof(S) == 4) {
-          *reinterpret_cast<float4*>(dst) =
-              float4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-        } else {
-          const uint32_t lo = uint32_t(Traits<T>::from_float(acc[i][j][4 * g])) |
-                              (uint32_t(Traits<T>::from_float(acc[i][j][4 * g + 1])) << 16);
-          const uint32_t hi = uint32_t(Traits<T>::from_float(acc[i][j][4 * g + 2])) |
-                              (uint32_t(Traits<T>::from_float(acc[i][j][4 * g + 3])) << 16);
-          *reinterpret_cast<uint2*>(dst) = uint2{lo, hi};
-        }
-      }
-    }
-    __syncthreads();
-    write_out<S, BN, WM, NT>(p, stage, m0 + i * 32, WTM, n0, boff_c, tid);
-    __syncthreads();
-  }
+  static_assert(epilogue_bytes<S, BM, BN, WM>() <= int(sizeof(lds)), "epilogue must fit in LDS");
+  store_tile<T, BM, BN, WM, WN>(p, lds, acc, m0, n0, boff_c);
 }
 
 // ---- launcher ----------------------------------------------------------------------
