@@ -289,3 +289,29 @@ def test_repeated_calls_replay_with_fresh_data_and_geometry(gpu):
     x = randn(6, 4, seed=44)
     for _ in range(2):
         assert_bitexact(es.einshard("h p -> (p h)", x.to(gpu)), x.t().reshape(-1))
+
+
+# ---- the 256 x 256 kernels (only chosen when they still give every CU a tile) -------
+
+
+@pytest.mark.parametrize(
+    "expr, shapes, kernel",
+    [
+        # K-contiguous operands: the software-pipelined kernel; ragged M and N,
+        # an odd (3) and an even (4) number of 64-deep K tiles
+        ("m k, n k -> m n", [(4136, 192), (4072, 192)], "contract_pipe_256x256"),
+        ("m k, n k -> m n", [(4096, 256), (4200, 256)], "contract_pipe_256x256"),
+        # two K sub-axes (the inner one exactly one K tile), batch offsets
+        ("m a k, n a k -> m n", [(4096, 3, 64), (4096, 3, 64)], "contract_pipe_256x256"),
+        ("b m k, b n k -> b m n", [(16, 1024, 128), (16, 1000, 128)], "contract_pipe_256x256"),
+        # an M-contiguous operand: the 8-wave kernel at 256 x 256
+        ("k m, n k -> m n", [(128, 4096), (4096, 128)], "contract_256x256"),
+    ],
+)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_large_tiles(gpu, expr, shapes, kernel, dtype):
+    x = randn(*shapes[0], seed=71, dtype=dtype)
+    y = randn(*shapes[1], seed=72, dtype=dtype)
+    got = es.einshard(expr, x.to(gpu), y.to(gpu))
+    assert _native.last_kernel() == kernel
+    assert_rel(got, einshard_cpu(expr, x, y), TOL[dtype])

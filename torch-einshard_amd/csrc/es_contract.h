@@ -7,10 +7,10 @@
 // in place: the tile loaders turn a tile index into addresses, no transposed
 // copy is ever materialised.
 //
-// Work-group: WM x WN waves own a BM x BN output tile; the K loop walks BK-deep
-// slabs through double-buffered LDS (one barrier per slab).  LDS keeps both
-// tiles K-contiguous ([row][k], row pitch BK + 16 bytes) so one 16-byte
-// ds_read per lane feeds one MFMA fragment:
+// LDS tiles hold 128-byte rows of K (BK = 64 for 16-bit types, 32 for f32) with the
+// 16-byte chunk c of row r stored at chunk position c ^ ((r / 2) % 8), so fragment
+// reads (32 consecutive rows, one chunk) and tile writes are free of bank conflicts.
+// A 16-byte ds_read gives a lane one MFMA fragment:
 //   * bf16/f16: v_mfma_f32_32x32x16 — lane l holds k = 8*(l/32) .. +7 of row l%32;
 //   * f32:      v_mfma_f32_32x32x2  — a 16-byte read gives a lane 4 consecutive
 //     k; four MFMAs consume them, lanes 0-31 supplying k 0..3 and lanes 32-63
@@ -18,15 +18,22 @@
 //     A[m,k]*B[n,k] is formed exactly once (only the summation order differs).
 // The MFMA's first operand is the N-side fragment and the second the M-side
 // one, so the accumulator holds C^T: each lane ends with 4 consecutive n of
-// one m.  The epilogue stages 32-row slices of the tile in LDS and writes
-// them with 16-byte stores along n when n is the output's contiguous axis.
+// one m.  The epilogue computes every tile row's and column's output offset once
+// into LDS tables, stages 32-row slices of the tile in LDS and writes them with
+// 16-byte stores along n when n is the output's contiguous axis.
 //
-// Global -> LDS loaders (per operand):
-//   * K-contiguous: 16-byte loads along k, stored as-is;
-//   * MN-contiguous: a thread loads a VEC(k) x VEC(m) block with 16-byte loads
-//     along m and transposes it in registers (v_perm_b32 for 16-bit types)
-//     before 16-byte LDS stores;
-//   * generic: element loads with full index decomposition (any strides).
+// Kernels:
+//   * contract_pipe (16-bit types, both operands K-contiguous, 256 x 256 tiles):
+//     4 waves of 128 x 128, two LDS stages filled by global_load_lds_dwordx4
+//     copies issued a full K tile ahead, an explicit MFMA / LDS-read / copy
+//     interleave (see es_contract_kernel.h);
+//   * contract_kernel (every other case): WM x WN waves over a BM x BN tile,
+//     double-buffered LDS with one barrier per K tile.  Its loaders:
+//       - K-contiguous: direct global -> LDS copies;
+//       - MN-contiguous: a thread loads a VEC(k) x VEC(m) block with 16-byte loads
+//         along m and transposes it in registers (v_perm_b32 for 16-bit types)
+//         before 16-byte LDS stores;
+//       - generic: element loads with full index decomposition (any strides).
 #pragma once
 
 #include "es_common.h"
@@ -51,6 +58,7 @@ struct ContractArgs {
   uint32_t tiles_m, tiles_n;
   uint32_t total_tiles;
   int32_t vstore;        // 16-byte vector stores along n
+  int32_t off32;         // every byte offset into A and B fits in 32 bits
   uint32_t k_inner;      // extent of the innermost K sub-axis (fast paths: a multiple of BK)
   int64_t ka_inner;      // stride of the innermost K sub-axis in A
   int64_t kb_inner;      // ... in B

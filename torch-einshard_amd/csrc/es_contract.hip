@@ -31,6 +31,21 @@ int fill_group(GroupArgs& g, int n, const es_axis* axes, uint64_t& extent, const
   return ES_OK;
 }
 
+// largest byte offset of an operand: sum over its axes of (size - 1) * |stride|
+uint64_t max_offset_bytes(const es_contract_desc* d, int which, int esz) {
+  uint64_t off = 0;
+  auto add = [&](const es_axis* axes, int n) {
+    for (int i = 0; i < n; ++i) {
+      const int64_t st = which == 0 ? axes[i].a : axes[i].b;
+      if (axes[i].size > 0) off += uint64_t(axes[i].size - 1) * uint64_t(st < 0 ? -st : st);
+    }
+  };
+  add(d->batch, d->n_batch);
+  add(which == 0 ? d->m : d->n, which == 0 ? d->n_m : d->n_n);
+  add(d->k, d->n_k);
+  return off * uint64_t(esz);
+}
+
 bool strides_multiple(const es_axis* axes, int n, int skip_last, int which, int64_t q) {
   for (int i = 0; i < n - skip_last; ++i) {
     const int64_t s = which == 0 ? axes[i].a : (which == 1 ? axes[i].b : axes[i].c);
@@ -104,6 +119,7 @@ extern "C" int es_contract(const es_contract_desc* d, const void* a, const void*
   if (d->n_k > 2) la = lb = kGeneric;
   p.ka_outer = d->n_k == 2 ? d->k[0].a : int64_t(p.k_inner) * p.ka_inner;
   p.kb_outer = d->n_k == 2 ? d->k[0].b : int64_t(p.k_inner) * p.kb_inner;
+  p.off32 = max_offset_bytes(d, 0, esz) + 16 < (uint64_t(1) << 32) && max_offset_bytes(d, 1, esz) + 16 < (uint64_t(1) << 32);
   p.vstore = 0;
   if (d->n_n > 0) {
     const es_axis& nin = d->n[d->n_n - 1];

@@ -574,6 +574,240 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const Contrac
   store_tile<T, BM, BN, WM, WN>(p, lds, acc, m0, n0, boff_c);
 }
 
+// ---- software-pipelined 256 x 256 kernel, both operands K-contiguous ------------
+// Four waves (2 x 2), each owning a 128 x 128 block: per 16-deep k step a wave reads
+// 8 fragments for 16 MFMAs, half the LDS reads per MFMA of the 8-wave kernel.  With
+// one wave per SIMD nothing hides a stall, so the schedule is explicit:
+//   substeps 0 .. NS-2: 16 MFMAs interleaved with the fragment reads of the next
+//                       substep;
+//   barrier:            the K tile for step kt+1 has landed (own copies: vmcnt(0);
+//                       everyone's: the barrier) and nobody reads stage kt any more;
+//   substep NS-1:       16 MFMAs interleaved with the copies of K tile kt+2 into
+//                       stage kt (issued a full step before they are needed) and the
+//                       fragment reads of step kt+1's first substep.
+// The loop body has no branches: past the last tile the copies re-fetch the last tile
+// into a stage nobody reads.
+struct PipeWalk {
+  uint32_t t;     // K tile index of the next copy
+  uint32_t kin;   // position inside the innermost K sub-axis
+  int64_t oa, ob; // element offsets of that tile in A and B
+  int64_t da0, db0, da1, db1;  // advance inside the inner sub-axis / across its end
+
+  __device__ __forceinline__ void start(const ContractArgs& p, int bk) {
+    t = 0;
+    kin = 0;
+    oa = ob = 0;
+    da0 = int64_t(bk) * p.ka_inner;
+    db0 = int64_t(bk) * p.kb_inner;
+    da1 = da0 + p.ka_outer - int64_t(p.k_inner) * p.ka_inner;
+    db1 = db0 + p.kb_outer - int64_t(p.k_inner) * p.kb_inner;
+  }
+  // next tile, or stay on the last one
+  __device__ __forceinline__ void advance(const ContractArgs& p, uint32_t nk, int bk) {
+    const bool step = t + 1 < nk;
+    const uint32_t kin2 = kin + uint32_t(bk);
+    const bool wrap = kin2 == p.k_inner;
+    oa += step ? (wrap ? da1 : da0) : 0;
+    ob += step ? (wrap ? db1 : db0) : 0;
+    kin = step ? (wrap ? 0u : kin2) : kin;
+    t += step ? 1u : 0u;
+  }
+};
+
+// One 1 KB global -> LDS copy: lane l moves 16 bytes from sbase + voff into LDS byte
+// address lds + 16 * l (global_load_lds_dwordx4, scalar-base form).  Issued as inline
+// assembly: the compiler then keeps the per-lane offset in one loop-invariant register
+// (instead of a 64-bit address it may reuse while the copy still reads it) and does not
+// order LDS reads behind the copy; the kernel orders them with explicit
+// s_waitcnt vmcnt and barriers.  M0 carries the LDS address; nothing else in the
+// kernels that use it touches M0.
+__device__ __forceinline__ void copy_to_lds(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return uint32_t(uintptr_t((const lds_void*)p));
+}
+
+// Copies of a K-contiguous tile for contract_pipe: 32-bit byte offsets of this lane's
+// rows from a scalar base (the operand pointer plus the K tile's offset), so each copy
+// is one global_load_lds_dwordx4 with a scalar base address.  The host guarantees
+// that every offset of the operand fits in 32 bits.
+template <typename S, int ROWS, int NW, int SIDE>
+struct PipeCopies {
+  static constexpr int RPI = 64 / kChunks;  // rows per copy instruction
+  static constexpr int NI = ROWS / RPI / NW;
+  static_assert(NI >= 1 && ROWS % (RPI * NW) == 0, "tile shape");
+  uint32_t off[NI];
+  int region0;
+
+  __device__ __forceinline__ void init(const ContractArgs& p, int wave, int lane, uint32_t row0, int64_t boff) {
+    region0 = wave * NI;
+    const GroupArgs& g = SIDE == 0 ? p.gm : p.gn;
+    const uint32_t lim = (SIDE == 0 ? p.M : p.N) - 1;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = (region0 + i) * RPI + lane / kChunks;
+      const int chunk = swz(row, lane % kChunks);
+      uint32_t r = row0 + row;
+      r = r > lim ? lim : r;  // rows past the edge re-read the last row; never stored
+      off[i] = uint32_t((boff + group_offset<SIDE>(g, r)) * int64_t(sizeof(S))) + uint32_t(chunk * 16);
+    }
+  }
+  // copy i of this wave's share of the tile at `base` into the LDS tile at byte address `lds`
+  __device__ __forceinline__ void issue_one(int i, const void* base, uint32_t lds) const {
+    copy_to_lds(base, off[i], lds + uint32_t((region0 + i) * 1024));
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
+  using S = typename Traits<T>::S;
+  constexpr int BM = 256, BN = 256, WM = 2, WN = 2, NT = 256;
+  constexpr int VEC = Traits<T>::VEC;
+  constexpr int BK = kRowBytes / int(sizeof(S));
+  constexpr int KSTEP = 2 * VEC;
+  constexpr int NS = BK / KSTEP;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int MMA_PER_FRAG = sizeof(S) == 4 ? 4 : 1;  // MFMA instructions per fragment pair
+  constexpr int MMAS = FM * FN * MMA_PER_FRAG;          // per substep
+  using CopyA = PipeCopies<S, BM, WM * WN, 0>;
+  using CopyB = PipeCopies<S, BN, WM * WN, 1>;
+  constexpr int NCOPY = CopyA::NI + CopyB::NI;  // copies per wave per K tile
+  static_assert(NS % 2 == 0, "fragment double buffer alternates within a step");
+  static_assert(epilogue_bytes<S, BM, BN, WM>() <= int(sizeof(S)) * STAGE, "epilogue must fit in one stage");
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0, "fragment rows of a lane share one swizzle key");
+
+  // two stages as two arrays: the compiler can then tell the copies into one from
+  // the fragment reads of the other and does not wait for the copies before reading
+  __shared__ __attribute__((aligned(1024))) S lds0[STAGE];
+  __shared__ __attribute__((aligned(1024))) S lds1[STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % 64;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+
+  uint32_t bid = blockIdx.x;
+  if (p.total_tiles % 8 == 0) bid = (bid % 8) * (p.total_tiles / 8) + bid / 8;
+  const uint32_t per_batch = p.tiles_m * p.tiles_n;
+  const uint32_t bidx = bid / per_batch;
+  const uint32_t rem = bid - bidx * per_batch;
+  const uint32_t tm = rem / p.tiles_n;
+  const uint32_t tn = rem - tm * p.tiles_n;
+  const uint32_t m0 = tm * BM;
+  const uint32_t n0 = tn * BN;
+  const int64_t boff_a = group_offset<0>(p.gb, bidx);
+  const int64_t boff_b = group_offset<1>(p.gb, bidx);
+  const int64_t boff_c = group_offset<2>(p.gb, bidx);
+
+  CopyA ca;
+  CopyB cb;
+  ca.init(p, wave, lane, m0, boff_a);
+  cb.init(p, wave, lane, n0, boff_b);
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // Fragment addressing.  Fragment rows of this lane are lane % 32 plus multiples of
+  // 16, so they share the swizzle key ((row / 2) % 8): the chunk position of k-chunk
+  // 2 * ks + lane / 32 is the same for all of them, and a fragment's address is a
+  // per-substep lane offset plus a compile-time row offset.
+  const int lrow = lane % 32;
+  int kofs[NS];
+#pragma unroll
+  for (int ks = 0; ks < NS; ++ks) kofs[ks] = lrow * BK + swz(lrow, ks * 2 + lane / 32) * VEC;
+  const int abase = wm * WTM * BK;
+  const int bbase = BM * BK + wn * WTN * BK;
+
+  uint4 af[2][FM], bf[2][FN];
+  auto frags = [&](const S* stage, int buf, int ks) {
+    const S* a = stage + abase + kofs[ks];
+    const S* b = stage + bbase + kofs[ks];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const uint4*>(a + i * 32 * BK);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[buf][j] = *reinterpret_cast<const uint4*>(b + j * 32 * BK);
+  };
+  auto mmas = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) Traits<T>::mma(acc[i][j], bf[buf][j], af[buf][i]);
+  };
+
+  const uint32_t nk = (p.K + BK - 1) / BK;  // >= 1: an empty K takes the generic kernel
+  PipeWalk w;
+  w.start(p, BK);
+  const uint32_t lds0_addr = lds_address(lds0);
+  const uint32_t lds1_addr = lds_address(lds1);
+  // copy q (0 .. NCOPY-1) of the tile the walk points at into the stage at `stage`
+  auto copy = [&](int q, uint32_t stage) {
+    if (q < CopyA::NI) ca.issue_one(q, static_cast<const S*>(p.a) + w.oa, stage);
+    else cb.issue_one(q - CopyA::NI, static_cast<const S*>(p.b) + w.ob, stage + uint32_t(BM * BK * sizeof(S)));
+  };
+#pragma unroll
+  for (int q = 0; q < NCOPY; ++q) copy(q, lds0_addr);
+  w.advance(p, nk, BK);
+#pragma unroll
+  for (int q = 0; q < NCOPY; ++q) copy(q, lds1_addr);
+  w.advance(p, nk, BK);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY) : "memory");  // tile 0 of this wave landed
+  __syncthreads();
+  frags(lds0, 0, 0);
+
+  // one K tile: stage_cur holds it, stage_nxt the next one
+  auto step = [&](S* stage_cur, const S* stage_nxt, uint32_t cur_addr) {
+#pragma unroll
+    for (int ks = 0; ks + 1 < NS; ++ks) {
+      frags(stage_cur, (ks + 1) & 1, ks + 1);
+      mmas(ks & 1);
+#pragma unroll
+      for (int q = 0; q < MMAS; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                    // one MFMA
+        if (q < FM + FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      }
+      __builtin_amdgcn_sched_barrier(0);  // substeps are scheduled one at a time
+    }
+    // tile kt+1 complete for everyone; every read of stage kt done
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    // last substep: its MFMAs, the copies of tile kt+2 into this stage and the first
+    // fragments of tile kt+1, interleaved in program order
+    {
+      constexpr int buf = (NS - 1) & 1;
+#pragma unroll
+      for (int q = 0; q < FM * FN; ++q) {
+        Traits<T>::mma(acc[q / FN][q % FN], bf[buf][q % FN], af[buf][q / FN]);
+        if (q < NCOPY) copy(q, cur_addr);
+        if (q < FM) af[0][q] = *reinterpret_cast<const uint4*>(stage_nxt + abase + kofs[0] + q * 32 * BK);
+        else if (q < FM + FN) bf[0][q - FM] = *reinterpret_cast<const uint4*>(stage_nxt + bbase + kofs[0] + (q - FM) * 32 * BK);
+      }
+#pragma unroll
+      for (int q = FM * FN; q < NCOPY; ++q) copy(q, cur_addr);
+      w.advance(p, nk, BK);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  uint32_t kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    step(lds0, lds1, lds0_addr);
+    step(lds1, lds0, lds1_addr);
+  }
+  if (kt < nk) step(lds0, lds1, lds0_addr);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  store_tile<T, BM, BN, WM, WN>(p, lds0, acc, m0, n0, boff_c);
+}
+
 // ---- launcher ----------------------------------------------------------------------
 template <typename T, int BM, int BN, int WM, int WN, int LA, int LB, int PF>
 int launch_one(const ContractArgs& p, hipStream_t s, const char* name) {
@@ -584,7 +818,15 @@ int launch_one(const ContractArgs& p, hipStream_t s, const char* name) {
 
 template <typename T, int BM, int BN, int WM, int WN, int PF>
 int launch_layouts(const ContractArgs& p, int la, int lb, hipStream_t s, const char* name) {
-  if (la == kKContig && lb == kKContig) return launch_one<T, BM, BN, WM, WN, kKContig, kKContig, PF>(p, s, name);
+  if (la == kKContig && lb == kKContig) {
+    if constexpr (BM == 256 && BN == 256 && sizeof(typename Traits<T>::S) == 2) {
+      if (!p.off32) return launch_one<T, BM, BN, WM, WN, kKContig, kKContig, PF>(p, s, name);
+      contract_pipe<T><<<p.total_tiles, 256, 0, s>>>(p);
+      set_kernel("contract_pipe_256x256");
+      return check_launch("es_contract");
+    }
+    return launch_one<T, BM, BN, WM, WN, kKContig, kKContig, PF>(p, s, name);
+  }
   if (la == kKContig && lb == kMNContig) return launch_one<T, BM, BN, WM, WN, kKContig, kMNContig, PF>(p, s, name);
   if (la == kMNContig && lb == kKContig) return launch_one<T, BM, BN, WM, WN, kMNContig, kKContig, PF>(p, s, name);
   if (la == kMNContig && lb == kMNContig) return launch_one<T, BM, BN, WM, WN, kMNContig, kMNContig, 1>(p, s, name);
