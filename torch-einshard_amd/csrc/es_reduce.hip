@@ -23,6 +23,11 @@ namespace {
 constexpr int kMax = ES_MAX_AXES;
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
+constexpr int kUnroll = 8;  // terms in flight per thread when unrolling
+// Unroll only grids with fewer threads than this: a larger grid keeps enough loads
+// in flight with one per thread, and spreading one thread's loads over distant
+// rows (a sum over a leading axis) was measured to slow it down.
+constexpr uint64_t kUnrollBelowThreads = uint64_t(1) << 21;
 
 template <typename S, int N>
 struct alignas(sizeof(S) * N) Pack {
@@ -38,6 +43,7 @@ struct ReduceArgs {
   uint32_t n_red;     // reduced index space
   uint32_t nsplit;    // work-group split of the reduced space
   uint32_t chunk;     // reduced indices per split
+  int32_t unroll;     // load kUnroll terms per thread before adding them
   int32_t n_keep;
   int32_t n_redax;
   FastDiv keep_div[kMax];  // column mode: innermost measured in vectors
@@ -92,41 +98,54 @@ __global__ __launch_bounds__(kThreads) void reduce_cols(const ReduceArgs p, cons
 
   const uint32_t r_begin = split * p.chunk;
   const uint32_t r_end = min(p.n_red, r_begin + p.chunk);
+  // term r of this thread: x (and y) at reduced index r
+  auto load = [&](uint32_t r, float (&xv)[VEC], float (&yv)[VEC]) {
+    int64_t rx, ry;
+    offsets(r, p.n_redax, p.red_div, p.red_sx, p.red_sy, rx, ry, 1);
+    const int64_t bx = kx + rx;
+    if constexpr (XMODE == 1) {
+      const Pack<S, VEC> v = *reinterpret_cast<const Pack<S, VEC>*>(x + bx);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) xv[i] = Elem<T>::load(v.v[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) xv[i] = Elem<T>::load(x[bx + i * ix]);
+    }
+    if constexpr (HAS_Y) {
+      const int64_t by = ky + ry;
+      if constexpr (YMODE == 1) {
+        const Pack<S, VEC> v = *reinterpret_cast<const Pack<S, VEC>*>(y + by);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) yv[i] = Elem<T>::load(v.v[i]);
+      } else if constexpr (YMODE == 0) {
+        const float s = Elem<T>::load(y[by]);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) yv[i] = s;
+      } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) yv[i] = Elem<T>::load(y[by + i * iy]);
+      }
+    }
+  };
+  auto add = [&](const float (&xv)[VEC], const float (&yv)[VEC]) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) acc[i] = HAS_Y ? fmaf(xv[i], yv[i], acc[i]) : acc[i] + xv[i];
+  };
   if (active) {
-    for (uint32_t r = r_begin + trow; r < r_end; r += waves) {
-      int64_t rx, ry;
-      offsets(r, p.n_redax, p.red_div, p.red_sx, p.red_sy, rx, ry, 1);
-      float xv[VEC];
-      const int64_t bx = kx + rx;
-      if constexpr (XMODE == 1) {
-        const Pack<S, VEC> v = *reinterpret_cast<const Pack<S, VEC>*>(x + bx);
+    // kUnroll terms are loaded before any is added, so each thread keeps kUnroll
+    // loads in flight; they are still added in increasing r
+    uint32_t r = r_begin + trow;
+    for (; p.unroll && r + (kUnroll - 1) * waves < r_end; r += kUnroll * waves) {
+      float xv[kUnroll][VEC], yv[kUnroll][VEC];
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) xv[i] = Elem<T>::load(v.v[i]);
-      } else {
+      for (int u = 0; u < kUnroll; ++u) load(r + u * waves, xv[u], yv[u]);
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) xv[i] = Elem<T>::load(x[bx + i * ix]);
-      }
-      if constexpr (HAS_Y) {
-        const int64_t by = ky + ry;
-        float yv[VEC];
-        if constexpr (YMODE == 1) {
-          const Pack<S, VEC> v = *reinterpret_cast<const Pack<S, VEC>*>(y + by);
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) yv[i] = Elem<T>::load(v.v[i]);
-        } else if constexpr (YMODE == 0) {
-          const float s = Elem<T>::load(y[by]);
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) yv[i] = s;
-        } else {
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) yv[i] = Elem<T>::load(y[by + i * iy]);
-        }
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[i] = fmaf(xv[i], yv[i], acc[i]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[i] += xv[i];
-      }
+      for (int u = 0; u < kUnroll; ++u) add(xv[u], yv[u]);
+    }
+    for (; r < r_end; r += waves) {
+      float xv[VEC], yv[VEC];
+      load(r, xv, yv);
+      add(xv, yv);
     }
   }
 
@@ -175,12 +194,11 @@ __global__ __launch_bounds__(kThreads) void reduce_rows(const ReduceArgs p) {
   const uint32_t r_begin = split * p.chunk;
   const uint32_t r_end = min(n_rvec, r_begin + p.chunk);
   float acc = 0.f;
-  for (uint32_t r = r_begin + lane; r < r_end; r += 64) {
+  auto load = [&](uint32_t r, Pack<S, VEC>& xv, float (&yv)[VEC]) {
     int64_t rx, ry;
     offsets(r, p.n_redax, p.red_div, p.red_sx, p.red_sy, rx, ry, VEC);
-    const Pack<S, VEC> xv = *reinterpret_cast<const Pack<S, VEC>*>(x + kx + rx);
+    xv = *reinterpret_cast<const Pack<S, VEC>*>(x + kx + rx);
     if constexpr (HAS_Y) {
-      float yv[VEC];
       if constexpr (YMODE == 1) {
         const Pack<S, VEC> v = *reinterpret_cast<const Pack<S, VEC>*>(y + ky + ry);
 #pragma unroll
@@ -190,12 +208,30 @@ __global__ __launch_bounds__(kThreads) void reduce_rows(const ReduceArgs p) {
 #pragma unroll
         for (int i = 0; i < VEC; ++i) yv[i] = s;
       }
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) acc = fmaf(Elem<T>::load(xv.v[i]), yv[i], acc);
-    } else {
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) acc += Elem<T>::load(xv.v[i]);
     }
+  };
+  auto add = [&](const Pack<S, VEC>& xv, const float (&yv)[VEC]) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const float v = Elem<T>::load(xv.v[i]);
+      acc = HAS_Y ? fmaf(v, yv[i], acc) : acc + v;
+    }
+  };
+  // as in column mode: kUnroll loads in flight, added in increasing r
+  uint32_t r = r_begin + lane;
+  for (; p.unroll && r + (kUnroll - 1) * 64 < r_end; r += kUnroll * 64) {
+    Pack<S, VEC> xv[kUnroll];
+    float yv[kUnroll][VEC];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) load(r + u * 64, xv[u], yv[u]);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) add(xv[u], yv[u]);
+  }
+  for (; r < r_end; r += 64) {
+    Pack<S, VEC> xv;
+    float yv[VEC];
+    load(r, xv, yv);
+    add(xv, yv);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
@@ -229,6 +265,7 @@ struct Schedule {
   uint32_t nsplit = 1;
   uint32_t chunk = 0;
   uint32_t grid_x = 1;
+  bool unroll = false;
   int xmode = 2, ymode = 2;
   uint64_t n_out = 1, n_red = 1;
 };
@@ -277,6 +314,7 @@ int plan(const es_reduce_desc* d, const void* x, const void* y, void* out, Sched
       s.nsplit = uint32_t(nsplit);
       s.chunk = uint32_t((n_rvec + nsplit - 1) / nsplit);
       s.grid_x = uint32_t(groups);
+      s.unroll = groups * nsplit * kThreads < kUnrollBelowThreads;
       return ES_OK;
     }
   }
@@ -318,6 +356,7 @@ int plan(const es_reduce_desc* d, const void* x, const void* y, void* out, Sched
   s.nsplit = uint32_t(nsplit);
   s.chunk = uint32_t((s.n_red + nsplit - 1) / nsplit);
   s.grid_x = uint32_t(groups);
+  s.unroll = groups * nsplit * kThreads < kUnrollBelowThreads;
   return ES_OK;
 }
 
@@ -422,6 +461,7 @@ extern "C" int es_reduce(const es_reduce_desc* d, const void* x, const void* y, 
   p.n_red = uint32_t(s.n_red);
   p.nsplit = s.nsplit;
   p.chunk = s.chunk;
+  p.unroll = s.unroll ? 1 : 0;
   p.n_keep = d->n_keep;
   p.n_redax = d->n_red;
   for (int i = 0; i < kMax; ++i) {
