@@ -128,13 +128,24 @@ __device__ __forceinline__ OffT source_of(const GatherArgs& p, uint32_t v, bool&
 // fill element loads from offset 0, always valid, and discards it), so each
 // thread keeps kUnroll loads in flight.
 constexpr int kUnroll = 4;
+constexpr uint32_t kRun = 64;  // consecutive work-groups per XCD
 
 template <int VB, int R, typename OffT, int BOUNDARY>
 __global__ __launch_bounds__(kThreads) void gather_kernel(const GatherArgs p) {
   using V = typename Vec<VB>::type;
   const uint32_t chunk = kUnroll * kThreads;
   const V fillv = fill_vec<VB>(p.fill);
-  for (uint32_t base = blockIdx.x * chunk; base < p.total; base += gridDim.x * chunk) {
+  // Work-groups are dealt to the 8 XCDs round robin.  Renumber them so each XCD
+  // walks runs of kRun consecutive work-groups: neighbouring outputs that re-read
+  // the same input rows (a window) then share one L2, while the 8 XCDs still
+  // stream through one narrow window of memory together (whole-output bands per
+  // XCD measured slower).
+  uint32_t blk = blockIdx.x;
+  if (gridDim.x % (8 * kRun) == 0) {
+    const uint32_t xcd = blk % 8, i = blk / 8;
+    blk = (i / kRun) * 8 * kRun + xcd * kRun + i % kRun;
+  }
+  for (uint32_t base = blk * chunk; base < p.total; base += gridDim.x * chunk) {
     OffT src[kUnroll];
     bool keep[kUnroll];
 #pragma unroll
@@ -334,7 +345,9 @@ extern "C" int es_gather(const es_gather_desc* d, const void* x, void* out, void
     if (reach > 0x3fffffffLL || p.base < -0x3fffffffLL || p.base > 0x3fffffffLL) off32 = false;
   }
   const uint64_t per_group = uint64_t(kUnroll) * kThreads;
-  const uint64_t blocks64 = (total_vec + per_group - 1) / per_group;
+  uint64_t blocks64 = (total_vec + per_group - 1) / per_group;
+  // whole runs of kRun work-groups per XCD (the extra groups find no work)
+  if (blocks64 >= 8 * kRun) blocks64 = (blocks64 + 8 * kRun - 1) / (8 * kRun) * (8 * kRun);
   const uint32_t blocks = uint32_t(blocks64 > 1048576 ? 1048576 : blocks64);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (vb) {
