@@ -304,8 +304,10 @@ def test_repeated_calls_replay_with_fresh_data_and_geometry(gpu):
         # two K sub-axes (the inner one exactly one K tile), batch offsets
         ("m a k, n a k -> m n", [(4096, 3, 64), (4096, 3, 64)], "contract_pipe_256x256"),
         ("b m k, b n k -> b m n", [(16, 1024, 128), (16, 1000, 128)], "contract_pipe_256x256"),
-        # an M-contiguous operand: the 8-wave kernel at 256 x 256
-        ("k m, n k -> m n", [(128, 4096), (4096, 128)], "contract_256x256"),
+        # an M-contiguous operand: copied K-contiguous first, then the pipelined kernel
+        ("k m, n k -> m n", [(128, 4096), (4096, 128)], "contract_pipe_256x256"),
+        # both operands contiguous along M / N (the C2 pattern on both sides)
+        ("k m, k n -> m n", [(192, 4096), (192, 4136)], "contract_pipe_256x256"),
     ],
 )
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -315,3 +317,21 @@ def test_large_tiles(gpu, expr, shapes, kernel, dtype):
     got = es.einshard(expr, x.to(gpu), y.to(gpu))
     assert _native.last_kernel() == kernel
     assert_rel(got, einshard_cpu(expr, x, y), TOL[dtype])
+
+
+def test_large_tiles_f32_m_contiguous(gpu):
+    # fp32 keeps the 8-wave 256 x 256 kernel with its register-transposing loader
+    x, y = randn(128, 4096, seed=73), randn(4096, 128, seed=74)
+    got = es.einshard("k m, n k -> m n", x.to(gpu), y.to(gpu))
+    assert _native.last_kernel() == "contract_256x256"
+    assert_rel(got, einshard_cpu("k m, n k -> m n", x, y), TOL[torch.float32])
+
+
+def test_c2_pattern_repacks_one_operand(gpu):
+    # x is K-contiguous, y contiguous along its free axes: y alone is repacked
+    x = randn(64, 32, 128, 64, seed=75, dtype=torch.bfloat16)
+    y = randn(32, 64, 128, 16, seed=76, dtype=torch.bfloat16)
+    expr = "a b k c, b c l d -> k l d a"
+    got = es.einshard(expr, x.to(gpu), y.to(gpu))
+    assert _native.last_kernel() == "contract_pipe_256x256"
+    assert_rel(got, einshard_cpu(expr, x, y), TOL[torch.bfloat16])

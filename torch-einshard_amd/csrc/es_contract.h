@@ -56,6 +56,7 @@ struct ContractArgs {
   void* c;
   uint32_t M, N, K, batch;
   uint32_t tiles_m, tiles_n;
+  uint32_t group_n;      // N-tiles per tile group (divides tiles_n; see tile_of)
   uint32_t total_tiles;
   int32_t vstore;        // 16-byte vector stores along n
   int32_t off32;         // every byte offset into A and B fits in 32 bits

@@ -77,6 +77,28 @@ int operand_layout(const es_contract_desc* d, const void* ptr, int which, int ve
   return kGeneric;
 }
 
+// N-tiles per tile group (see tile_of in es_contract_kernel.h): each XCD owns
+// run = tiles / 8 consecutive logical tiles, a rectangle of group_n N-tiles by
+// run / group_n M-tiles when group_n divides tiles_n, run and tiles_m * group_n
+// divides into whole runs.  Pick the one touching the fewest A plus B panels.
+uint32_t group_width(uint64_t tiles_m, uint64_t tiles_n, uint64_t total) {
+  uint32_t best = uint32_t(tiles_n);  // N fastest over the whole row
+  if (total % 8 != 0) return best;
+  const uint64_t run = total / 8;
+  uint64_t best_cost = ~uint64_t(0);
+  for (uint64_t gn = 1; gn <= tiles_n; ++gn) {
+    if (tiles_n % gn != 0 || run % gn != 0) continue;
+    const uint64_t bm = run / gn;
+    if ((tiles_m * gn) % run != 0 || bm > tiles_m) continue;
+    const uint64_t cost = bm + gn;
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = uint32_t(gn);
+    }
+  }
+  return best;
+}
+
 }  // namespace
 }  // namespace es
 
@@ -148,6 +170,7 @@ extern "C" int es_contract(const es_contract_desc* d, const void* a, const void*
   p.tiles_m = uint32_t(tm);
   p.tiles_n = uint32_t(tn);
   p.total_tiles = uint32_t(total);
+  p.group_n = group_width(tm, tn, total);
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (d->dtype) {

@@ -127,6 +127,24 @@ struct KWalk {
   }
 };
 
+// ---- work-group -> tile ------------------------------------------------------------
+// The hardware deals work-groups to the 8 XCDs round robin.  Work-group b is given
+// logical tile (b % 8) * (tiles / 8) + b / 8, so each XCD owns a contiguous run of
+// logical tiles; logical tiles walk groups of group_n N-tiles, M fastest inside a
+// group, so that run is a compact rectangle of group_n N-tiles by run / group_n
+// M-tiles and the XCD's L2 sees few distinct A and B panels.
+__device__ __forceinline__ void tile_of(const ContractArgs& p, uint32_t b, uint32_t& bidx, uint32_t& tm, uint32_t& tn) {
+  if (p.total_tiles % 8 == 0) b = (b % 8) * (p.total_tiles / 8) + b / 8;
+  const uint32_t per_batch = p.tiles_m * p.tiles_n;
+  bidx = b / per_batch;
+  const uint32_t rem = b - bidx * per_batch;
+  const uint32_t gsize = p.tiles_m * p.group_n;  // tiles per group
+  const uint32_t g = rem / gsize;
+  const uint32_t r = rem - g * gsize;
+  tm = r / p.group_n;
+  tn = g * p.group_n + (r - tm * p.group_n);
+}
+
 // ---- tile loaders -------------------------------------------------------------
 // SIDE 0 loads the M-side tile from A, SIDE 1 the N-side tile from B.
 template <typename T, int ROWS, int BK, int NT, int LAYOUT, int SIDE>
@@ -425,13 +443,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const Contrac
   // work-group -> tile.  The hardware deals work-groups to the 8 XCDs round
   // robin; give each XCD a contiguous run of tiles (N fastest) so tiles that
   // share an M panel of A meet in the same L2.
-  uint32_t bid = blockIdx.x;
-  if (p.total_tiles % 8 == 0) bid = (bid % 8) * (p.total_tiles / 8) + bid / 8;
-  const uint32_t per_batch = p.tiles_m * p.tiles_n;
-  const uint32_t bidx = bid / per_batch;
-  const uint32_t rem = bid - bidx * per_batch;
-  const uint32_t tm = rem / p.tiles_n;
-  const uint32_t tn = rem - tm * p.tiles_n;
+  uint32_t bidx, tm, tn;
+  tile_of(p, blockIdx.x, bidx, tm, tn);
   const uint32_t m0 = tm * BM;
   const uint32_t n0 = tn * BN;
 
@@ -691,13 +704,8 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   const int wm = wave / WN;
   const int wn = wave % WN;
 
-  uint32_t bid = blockIdx.x;
-  if (p.total_tiles % 8 == 0) bid = (bid % 8) * (p.total_tiles / 8) + bid / 8;
-  const uint32_t per_batch = p.tiles_m * p.tiles_n;
-  const uint32_t bidx = bid / per_batch;
-  const uint32_t rem = bid - bidx * per_batch;
-  const uint32_t tm = rem / p.tiles_n;
-  const uint32_t tn = rem - tm * p.tiles_n;
+  uint32_t bidx, tm, tn;
+  tile_of(p, blockIdx.x, bidx, tm, tn);
   const uint32_t m0 = tm * BM;
   const uint32_t n0 = tn * BN;
   const int64_t boff_a = group_offset<0>(p.gb, bidx);

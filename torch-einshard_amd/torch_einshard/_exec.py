@@ -1,18 +1,21 @@
 """Run planned operations on the GPU through libeinshard_hip.
 
 Every function here takes device tensors, allocates the (dense) output with
-``torch.empty`` and enqueues exactly one library entry point on the current
-stream.  Tensors are passed by data pointer plus element strides; nothing is
-copied or made contiguous on the host side.
+``torch.empty`` and enqueues one library entry point on the current stream —
+preceded, for a large 16-bit contraction whose operand is contiguous along M or
+N, by one es_gather that copies that operand K-contiguous into a temporary.
+Tensors are passed by data pointer plus element strides; nothing is copied or
+made contiguous on the host side.
 """
 
 import ctypes
+from dataclasses import replace
 
 import torch
 
 from . import _native
 from ._native import MAX_AXES, BcastDesc, ContractDesc, GatherDesc, ReduceDesc, call
-from .planner import BcastOp, ContractOp, EmptyOp, GatherOp, ReduceOp
+from .planner import BcastOp, ContractOp, EmptyOp, GatherOp, ReduceOp, dense_strides
 
 __all__ = ["check_device_tensors", "run_op", "run_gather", "dtype_code", "fill_bits", "Prepared", "prepare_op", "launch"]
 
@@ -67,11 +70,14 @@ def _set_axes(array, axes, what):
 class Prepared:
     """One planned launch.  The descriptor is built (and the reduction workspace
     size queried) once; a call then only allocates the output and binds data
-    pointers, so a repeated expression costs one ctypes call on the host."""
+    pointers, so a repeated expression costs one ctypes call on the host.
 
-    __slots__ = ("entry", "desc", "ref", "out_shape", "order", "workspace", "noop")
+    ``repack`` lists operands first copied into a dense temporary by es_gather:
+    (operand index, gather descriptor, temporary shape)."""
 
-    def __init__(self, entry, desc, out_shape, order, workspace=0, noop=False):
+    __slots__ = ("entry", "desc", "ref", "out_shape", "order", "workspace", "noop", "repack")
+
+    def __init__(self, entry, desc, out_shape, order, workspace=0, noop=False, repack=()):
         self.entry = entry
         self.desc = desc
         self.ref = ctypes.byref(desc) if desc is not None else None
@@ -79,6 +85,7 @@ class Prepared:
         self.order = order
         self.workspace = workspace
         self.noop = noop
+        self.repack = tuple((index, desc_, ctypes.byref(desc_), shape) for index, desc_, shape in repack)
 
 
 def _raw_stream(device):
@@ -93,6 +100,14 @@ def launch(prep, xs, device, dtype):
     handle = _native.lib()
     fn = getattr(handle, prep.entry)
     stream = _raw_stream(device)
+    if prep.repack:
+        xs = list(xs)
+        for index, _, ref, shape in prep.repack:
+            tmp = torch.empty(shape, dtype=xs[index].dtype, device=device)
+            status = handle.es_gather(ref, xs[index].data_ptr(), tmp.data_ptr(), stream)
+            if status < 0:
+                raise _native.NativeError("es_gather", status, handle.es_last_error().decode())
+            xs[index] = tmp
     ptrs = [xs[i].data_ptr() for i in prep.order]
     if prep.entry == "es_reduce":
         need = prep.workspace
@@ -111,6 +126,66 @@ def _ptr(tensor):
 
 def run_gather(desc, x, out):
     call("es_gather", ctypes.byref(desc), _ptr(x), _ptr(out), _native.stream_of(out))
+
+
+# The 256 x 256 contraction kernel for 16-bit types needs both operands K-contiguous
+# (innermost K sub-axis of unit stride, a whole number of 64-deep K tiles).  When it
+# would be chosen (enough tiles for every CU) and an operand is instead contiguous
+# along M or N, that operand is first copied K-contiguous into a temporary: one
+# es_gather over its bytes buys the faster kernel.
+_BIG_TILE = 256
+_CU_TILES = 256
+_K_TILE_BYTES = 128
+
+
+def _prod(values):
+    out = 1
+    for v in values:
+        out *= v
+    return out
+
+
+def _repack_for_k_contiguity(op, order, elem_size):
+    if elem_size != 2 or not op.k or not op.m or not op.n:
+        return op, ()
+    tiles = _prod(a.size for a in op.batch)
+    tiles *= -(-_prod(a.size for a in op.m) // _BIG_TILE) * -(-_prod(a.size for a in op.n) // _BIG_TILE)
+    if tiles < _CU_TILES:
+        return op, ()
+    k_tile = _K_TILE_BYTES // elem_size
+    repack = []
+    for field, rows, index in (("a", op.m, order[0]), ("b", op.n, order[1])):
+        k_ok = getattr(op.k[-1], field) == 1 and op.k[-1].size % k_tile == 0
+        rows_inner = getattr(rows[-1], field) == 1
+        if k_ok or not rows_inner:
+            continue
+        axes = list(op.batch) + list(rows) + list(op.k)
+        if len(axes) > MAX_AXES:
+            continue
+        shape = tuple(a.size for a in axes)
+        dense = dense_strides(shape)
+        desc = GatherDesc()
+        desc.elem_size = elem_size
+        desc.boundary = 0
+        desc.fill_bits = 0
+        desc.out_rank = desc.in_rank = len(axes)
+        for i, axis in enumerate(axes):
+            desc.out_size[i] = desc.in_size[i] = axis.size
+            desc.in_stride[i] = getattr(axis, field)
+            desc.offset[i] = 0
+            desc.pos[i] = i
+            desc.win[i] = -1
+        repack.append((index, desc, shape))
+        nb, nr = len(op.batch), len(rows)
+
+        def restride(group, start, field=field, dense=dense):
+            return [replace(axis, **{field: dense[start + i]}) for i, axis in enumerate(group)]
+
+        batch = restride(op.batch, 0)
+        new_rows = restride(rows, nb)
+        k = restride(op.k, nb + nr)
+        op = replace(op, batch=batch, k=k, **({"m": new_rows} if field == "a" else {"n": new_rows}))
+    return op, tuple(repack)
 
 
 def prepare_op(op, dtype, elem_size):
@@ -163,13 +238,15 @@ def prepare_op(op, dtype, elem_size):
         return Prepared("es_reduce", desc, op.out_shape, (0, 1 if op.has_y else 0), workspace=need)
 
     if isinstance(op, ContractOp):
+        order = (1, 0) if op.swapped else (0, 1)
+        op, repack = _repack_for_k_contiguity(op, order, elem_size)
         desc = ContractDesc()
         desc.dtype = code
         desc.n_batch = _set_axes(desc.batch, op.batch, "einshard")
         desc.n_m = _set_axes(desc.m, op.m, "einshard")
         desc.n_n = _set_axes(desc.n, op.n, "einshard")
         desc.n_k = _set_axes(desc.k, op.k, "einshard")
-        return Prepared("es_contract", desc, op.out_shape, (1, 0) if op.swapped else (0, 1))
+        return Prepared("es_contract", desc, op.out_shape, order, repack=repack)
 
     raise TypeError(f"unknown planned op {type(op).__name__}")
 
