@@ -106,6 +106,9 @@ def parse(expression):
     if tokens[i] != "->":
         raise ValueError(f"oracle parser: expected '->' in {expression!r}")
     out, i = _parse_tensor(tokens, i + 1)
+    # the reference grammar needs at least one axis per tensor (grammar.py:18)
+    if not out[0] or any(not spec[0] for spec in inputs):
+        raise ValueError(f"oracle parser: a tensor without axes in {expression!r}")
     return inputs, out
 
 

@@ -17,6 +17,7 @@ import torch.nn.functional as F
 from oracle import PINNING
 from oracle.brute import brute_einsum, brute_window, numpy_einsum_f64
 from oracle.einshard_oracle import einhalo_cpu, einshard_cpu, einwindow_cpu, equation
+from oracle.einshard_oracle import parse as oracle_parse
 
 from conftest import randn
 
@@ -196,3 +197,9 @@ def test_planted_window_offset_is_caught():
     got = einwindow_cpu("b h c -> b h kh c", x, {"h": "kh"}, {"h": 1})
     off_by_one = brute_window(x, list(got.shape), [0, 1, 3], [-1, 2, -1], [0, 0, 0])
     assert not torch.equal(got, off_by_one)
+
+
+def test_oracle_parser_rejects_a_tensor_without_axes():
+    # reference tests/test_grammar.py:142 and :199 expect "a b ->" to fail
+    with pytest.raises(ValueError):
+        oracle_parse("a b ->")

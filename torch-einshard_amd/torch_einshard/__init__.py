@@ -10,6 +10,7 @@ device tensors; there is no CPU path and no fallback to ``torch.einsum``.
 from . import symbolic
 from ._cache import call_key, lookup, remember
 from ._exec import launch
+from .autograd import needs_grad
 from .distributed import distributed_1d
 from .einsum import einsum, equation_of, prepare_local
 from .families import cached_expand_axis_families
@@ -112,6 +113,10 @@ def _record_local_plan():
 
 
 def _execute_einshard(shard, xs, mesh, shapes, sizes, policy, key=None):
+    if local_operation(shard) and needs_grad(xs):
+        output = einsum(shard, *xs, sizes=sizes)  # differentiable path, not cached
+        _record_local_plan()
+        return output
     if local_operation(shard):
         prep, packed, device, dtype = prepare_local(shard, xs, sizes=sizes)
         out = launch(prep, xs, device, dtype)
@@ -138,7 +143,7 @@ def einshard(shard, *xs, mesh=None, shapes=None, sizes=None, families=None, opti
     # its prepared launch: no parsing, planning or descriptor building
     key = call_key("einshard", xs, mesh, shapes, shard, sizes, families) if isinstance(shard, str) else None
     hit = lookup(key)
-    if hit is not None:
+    if hit is not None and not needs_grad(xs):
         prep, packed = hit
         out = launch(prep, xs, xs[0].device, xs[0].dtype)
         _record_local_plan()
