@@ -335,3 +335,31 @@ def test_c2_pattern_repacks_one_operand(gpu):
     got = es.einshard(expr, x.to(gpu), y.to(gpu))
     assert _native.last_kernel() == "contract_pipe_256x256"
     assert_rel(got, einshard_cpu(expr, x, y), TOL[torch.bfloat16])
+
+
+# ---- transposes (pure permutations whose input unit-stride dim is not innermost) ----
+
+
+@pytest.mark.parametrize(
+    "expr, shape",
+    [
+        ("a b -> b a", (300, 200)),
+        ("b t c h w -> b t h w c", (2, 3, 40, 5, 70)),
+        ("a b c -> c a b", (33, 7, 129)),
+        ("a b c d -> b d c a", (65, 3, 4, 70)),
+    ],
+)
+@pytest.mark.parametrize("dtype", [torch.uint8, torch.bfloat16, torch.float32, torch.int64])
+def test_transposes_are_bitexact(gpu, expr, shape, dtype):
+    x = (randn(*shape, seed=81) * 50).to(dtype)
+    got = es.einshard(expr, x.to(gpu))
+    assert _native.last_kernel() == "gather_transpose"
+    assert_bitexact(got, einshard_cpu(expr, x))
+
+
+@pytest.mark.parametrize("shape", [(16, 24, 40), (8, 33, 64), (3, 5, 7)])
+def test_transposes_with_short_or_odd_dims(gpu, shape):
+    # short P (tile depth below 64) and sizes that are not whole vectors
+    for dtype in (torch.uint8, torch.bfloat16, torch.float32):
+        x = (randn(*shape, seed=82) * 50).to(dtype)
+        assert_bitexact(es.einshard("a p q -> a q p", x.to(gpu)), einshard_cpu("a p q -> a q p", x))

@@ -193,6 +193,176 @@ void launch_vb(const GatherArgs& p, bool off32, int boundary, uint32_t blocks, h
   else launch_off<VB, int64_t>(p, boundary, blocks, s);
 }
 
+// ---- transposes -----------------------------------------------------------------
+// A pure permutation (every input dim read whole, once, by one output dim) whose
+// input unit-stride dim lands on an output dim P other than the innermost one Q
+// cannot be read and written with wide accesses at once.  A work-group moves a
+// TP x 64 tile of (P, Q) for one combination of the other dims through LDS: it
+// reads VEC-element vectors along P (contiguous in the input) and writes them
+// along Q (contiguous in the output).  TP adapts to a short P.
+constexpr int kTileQ = 64;
+
+struct TransposeArgs {
+  const unsigned char* x;
+  unsigned char* out;
+  uint32_t tiles_p, tiles_q, n_outer;
+  uint32_t size_p, size_q;
+  int64_t q_in_stride;   // elements
+  int64_t p_out_stride;  // elements (output is dense)
+  int32_t n_rest;        // other output dims, outermost first
+  FastDiv rest_div[kMax];
+  int64_t rest_in[kMax];   // input stride of each (elements)
+  int64_t rest_out[kMax];  // output stride of each (elements)
+};
+
+template <typename E, int VEC>
+struct EVec {
+  E v[VEC];
+};
+
+// VEC elements per access; the host guarantees that size_p and size_q are multiples
+// of VEC and that every vector is VEC-element aligned in both tensors.
+template <typename E, int VEC, int TP>
+__global__ __launch_bounds__(256) void transpose_kernel(const TransposeArgs a) {
+  using V = EVec<E, VEC>;
+  static_assert(TP % VEC == 0 && kTileQ % VEC == 0, "tile shape");
+  __shared__ E tile[kTileQ][TP + 1];
+  const E* x = reinterpret_cast<const E*>(a.x);
+  E* out = reinterpret_cast<E*>(a.out);
+  const uint32_t per_outer = a.tiles_p * a.tiles_q;
+  for (uint32_t b = blockIdx.x; b < per_outer * a.n_outer; b += gridDim.x) {
+    uint32_t outer = b / per_outer;
+    const uint32_t t = b - outer * per_outer;
+    const uint32_t tp = t / a.tiles_q, tq = t - tp * a.tiles_q;
+    int64_t in_base = 0, out_base = 0;
+    for (int d = a.n_rest - 1; d >= 0; --d) {
+      uint32_t r;
+      outer = a.rest_div[d].divmod(outer, r);
+      in_base += int64_t(r) * a.rest_in[d];
+      out_base += int64_t(r) * a.rest_out[d];
+    }
+    const uint32_t p0 = tp * TP, q0 = tq * kTileQ;
+    // read: vectors along P, one row of the tile per q
+    constexpr int RV = TP / VEC;  // vectors per q row
+    for (int v = threadIdx.x; v < kTileQ * RV; v += 256) {
+      const int q = v / RV, pv = (v - q * RV) * VEC;
+      if (p0 + pv < a.size_p && q0 + q < a.size_q) {
+        const V val = *reinterpret_cast<const V*>(x + in_base + int64_t(q0 + q) * a.q_in_stride + p0 + pv);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) tile[q][pv + e] = val.v[e];
+      }
+    }
+    __syncthreads();
+    // write: vectors along Q, one output row per p
+    constexpr int WV = kTileQ / VEC;  // vectors per p row
+    for (int v = threadIdx.x; v < TP * WV; v += 256) {
+      const int p = v / WV, qv = (v - p * WV) * VEC;
+      if (p0 + p < a.size_p && q0 + qv < a.size_q) {
+        V val;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) val.v[e] = tile[qv + e][p];
+        *reinterpret_cast<V*>(out + out_base + int64_t(p0 + p) * a.p_out_stride + q0 + qv) = val;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <typename E, int VEC>
+void launch_transpose(const TransposeArgs& a, int tp, uint32_t blocks, hipStream_t s) {
+  switch (tp) {
+    // tp is at least VEC (the host rounds it up), so each instance sees TP >= VEC
+    case 8: transpose_kernel<E, VEC, (VEC > 8 ? VEC : 8)><<<blocks, 256, 0, s>>>(a); break;
+    case 16: transpose_kernel<E, VEC, (VEC > 16 ? VEC : 16)><<<blocks, 256, 0, s>>>(a); break;
+    case 32: transpose_kernel<E, VEC, 32><<<blocks, 256, 0, s>>>(a); break;
+    default: transpose_kernel<E, VEC, 64><<<blocks, 256, 0, s>>>(a); break;
+  }
+}
+
+// The transpose path of es_gather, or false when the descriptor is not such a transpose.
+bool try_transpose(const es_gather_desc* d, const void* x, void* out, hipStream_t s, int& status) {
+  const int rank = d->out_rank;
+  if (d->in_rank != rank || rank < 2) return false;
+  int feeder[kMax];
+  for (int i = 0; i < rank; ++i) feeder[i] = -1;
+  for (int j = 0; j < rank; ++j) {
+    const int p = d->pos[j];
+    if (d->win[j] >= 0 || d->offset[j] != 0 || d->in_size[j] != d->out_size[p] || feeder[p] >= 0) return false;
+    feeder[p] = j;
+  }
+  const int q = rank - 1;
+  int pdim = -1;
+  for (int i = 0; i < rank - 1; ++i)
+    if (d->in_stride[feeder[i]] == 1 && d->out_size[i] > 1) pdim = i;
+  if (pdim < 0 || d->in_stride[feeder[q]] == 1 || d->out_size[q] < kTileQ / 4) return false;
+  TransposeArgs a;
+  a.x = static_cast<const unsigned char*>(x);
+  a.out = static_cast<unsigned char*>(out);
+  a.size_p = uint32_t(d->out_size[pdim]);
+  a.size_q = uint32_t(d->out_size[q]);
+  a.tiles_q = (a.size_q + kTileQ - 1) / kTileQ;
+  a.q_in_stride = d->in_stride[feeder[q]];
+  int64_t dense[kMax];
+  int64_t run = 1;
+  for (int i = rank - 1; i >= 0; --i) {
+    dense[i] = run;
+    run *= d->out_size[i];
+  }
+  a.p_out_stride = dense[pdim];
+  a.n_rest = 0;
+  uint64_t n_outer = 1;
+  for (int i = 0; i < rank; ++i) {
+    if (i == pdim || i == q) continue;
+    a.rest_div[a.n_rest].init(uint32_t(d->out_size[i]));
+    a.rest_in[a.n_rest] = d->in_stride[feeder[i]];
+    a.rest_out[a.n_rest] = dense[i];
+    n_outer *= uint64_t(d->out_size[i]);
+    ++a.n_rest;
+  }
+  for (int i = a.n_rest; i < kMax; ++i) {
+    a.rest_div[i].init(1);
+    a.rest_in[i] = a.rest_out[i] = 0;
+  }
+  // 16-byte accesses when every vector is aligned and whole; element accesses otherwise
+  const int es_ = d->elem_size;
+  const int vec = 16 / es_;
+  bool wide = aligned(x, 16) && aligned(out, 16) && a.size_p % vec == 0 && a.size_q % vec == 0 &&
+              (a.q_in_stride * es_) % 16 == 0 && (a.p_out_stride * es_) % 16 == 0;
+  for (int i = 0; i < a.n_rest && wide; ++i)
+    if ((a.rest_in[i] * es_) % 16 != 0 || (a.rest_out[i] * es_) % 16 != 0) wide = false;
+  // tile depth along P: the power of two >= size_p, 8 .. 64, at least one vector
+  int tp = 8;
+  while (tp < 64 && uint32_t(tp) < a.size_p) tp *= 2;
+  if (wide && tp < vec) tp = vec;
+  a.tiles_p = (a.size_p + tp - 1) / tp;
+  const uint64_t blocks64 = n_outer * a.tiles_p * a.tiles_q;
+  if (blocks64 > kU32Max) return false;
+  a.n_outer = uint32_t(n_outer);
+  const uint32_t blocks = uint32_t(blocks64 > 1048576 ? 1048576 : blocks64);
+  hipStream_t st = s;
+  switch (es_) {
+    case 1:
+      if (wide) launch_transpose<uint8_t, 16>(a, tp, blocks, st);
+      else launch_transpose<uint8_t, 1>(a, tp, blocks, st);
+      break;
+    case 2:
+      if (wide) launch_transpose<uint16_t, 8>(a, tp, blocks, st);
+      else launch_transpose<uint16_t, 1>(a, tp, blocks, st);
+      break;
+    case 4:
+      if (wide) launch_transpose<uint32_t, 4>(a, tp, blocks, st);
+      else launch_transpose<uint32_t, 1>(a, tp, blocks, st);
+      break;
+    default:
+      if (wide) launch_transpose<uint64_t, 2>(a, tp, blocks, st);
+      else launch_transpose<uint64_t, 1>(a, tp, blocks, st);
+      break;
+  }
+  set_kernel("gather_transpose");
+  status = check_launch("es_gather");
+  return true;
+}
+
 }  // namespace
 }  // namespace es
 
@@ -235,6 +405,11 @@ extern "C" int es_gather(const es_gather_desc* d, const void* x, void* out, void
   for (int j = 0; j < d->in_rank; ++j) {
     const int64_t reach = d->out_size[d->pos[j]] - 1 + (d->win[j] >= 0 ? d->out_size[d->win[j]] - 1 : 0);
     checked[j] = d->win[j] >= 0 || d->offset[j] != 0 || reach + d->offset[j] >= d->in_size[j] || d->in_size[j] == 0;
+  }
+
+  {
+    int status = ES_OK;
+    if (try_transpose(d, x, out, static_cast<hipStream_t>(stream), status)) return status;
   }
 
   // widest vector: the innermost output dim must feed exactly one input dim,
