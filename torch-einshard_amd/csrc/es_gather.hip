@@ -16,6 +16,9 @@
 // Elements move as raw bits, so the copy is bit-exact for any element type.
 // The kernel is HBM-bound: each output byte is written once; a 3x3 window
 // re-reads each input element 9 times, from L2.
+#include <type_traits>
+#include <utility>
+
 #include "es_common.h"
 
 namespace es {
@@ -30,11 +33,11 @@ struct GatherArgs {
   uint64_t fill;  // fill pattern replicated over the vector width (low 8 bytes)
   uint32_t total; // number of output vectors
   int32_t out_rank;
-  int32_t inner_scale;  // elements per vector along the innermost output dim
+  int32_t inner_shift;  // log2 of the elements per vector along the innermost output dim
   int32_t nchk;         // range-checked input dims
   int64_t base;         // bytes: sum_j offset_j * stride_j
   FastDiv out_div[kMax];  // innermost dim measured in vectors
-  int64_t out_stride[kMax];  // bytes per unit of output coordinate d
+  int64_t out_stride[kMax];  // bytes per unit of output coordinate d (innermost: per vector)
   // range-checked input dims: coordinate = chk_off + sum_d (o[d] & chk_mask[k][d]),
   // chk_mask 0 or all ones (an output dim feeds an input dim at most once)
   int32_t chk_mask[kMax][kMax];
@@ -83,10 +86,20 @@ __device__ __forceinline__ V select_vec(bool keep, const V& a, const V& b) {
   }
 }
 
+// Quotient of n < 2^31 by f: the sum mulhi + n cannot carry out of 32 bits.
+__device__ __forceinline__ uint32_t div31(const FastDiv& f, uint32_t n) {
+  return (__umulhi(f.m, n) + n) >> f.l;
+}
+
 // Source byte offset of output vector v.  R is the (padded) output rank; OffT is
-// int32_t when every in-range source offset fits in 31 bits.  Branch-free: a
-// constant-boundary element outside the input only sets `outside`.
-template <int R, typename OffT, int BOUNDARY>
+// int32_t when every in-range source offset fits in 31 bits.  M24: the output
+// has fewer than 2^31 vectors and every dim size, quotient and byte stride fits
+// in 23 (strides 24) bits, so remainders and address terms come from full-rate
+// 24-bit multiply-adds (v_mad_i32_i24, v_mad_u32_u24) instead of quarter-rate
+// 32-bit multiplies; the wrapped 32-bit sum is exact since the result fits.
+// The outermost dim needs no division: v < total leaves its coordinate.
+// Branch-free: a constant-boundary element outside the input only sets `outside`.
+template <int R, typename OffT, int BOUNDARY, bool M24>
 __device__ __forceinline__ OffT source_of(const GatherArgs& p, uint32_t v, bool& outside) {
   int32_t coord[R];
   uint32_t rem = v;
@@ -94,10 +107,22 @@ __device__ __forceinline__ OffT source_of(const GatherArgs& p, uint32_t v, bool&
 #pragma unroll
   for (int d = R - 1; d >= 0; --d) {
     uint32_t r;
-    rem = p.out_div[d].divmod(rem, r);
-    if (d == R - 1) r *= uint32_t(p.inner_scale);
-    coord[d] = int32_t(r);
-    src += OffT(r) * OffT(p.out_stride[d]);
+    if (d == 0) {
+      r = rem;
+    } else if constexpr (M24) {
+      const uint32_t q = div31(p.out_div[d], rem);
+      r = uint32_t(__mul24(int32_t(q), -int32_t(p.out_div[d].d)) + int32_t(rem));
+      rem = q;
+    } else {
+      rem = p.out_div[d].divmod(rem, r);
+    }
+    // the innermost dim counts vectors: its coordinate in elements is r << inner_shift
+    coord[d] = d == R - 1 ? int32_t(r << p.inner_shift) : int32_t(r);
+    if constexpr (M24) {
+      src += OffT(__umul24(r, uint32_t(p.out_stride[d])));
+    } else {
+      src += OffT(r) * OffT(p.out_stride[d]);
+    }
   }
   outside = false;
   for (int k = 0; k < p.nchk; ++k) {
@@ -130,7 +155,7 @@ __device__ __forceinline__ OffT source_of(const GatherArgs& p, uint32_t v, bool&
 constexpr int kUnroll = 4;
 constexpr uint32_t kRun = 64;  // consecutive work-groups per XCD
 
-template <int VB, int R, typename OffT, int BOUNDARY>
+template <int VB, int R, typename OffT, int BOUNDARY, bool M24>
 __global__ __launch_bounds__(kThreads) void gather_kernel(const GatherArgs p) {
   using V = typename Vec<VB>::type;
   const uint32_t chunk = kUnroll * kThreads;
@@ -153,7 +178,7 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(const GatherArgs p) {
       const uint32_t v = base + u * kThreads + threadIdx.x;
       const bool valid = v < p.total;
       bool outside;
-      const OffT off = source_of<R, OffT, BOUNDARY>(p, valid ? v : 0u, outside);
+      const OffT off = source_of<R, OffT, BOUNDARY, M24>(p, valid ? v : 0u, outside);
       keep[u] = valid && !outside;
       src[u] = keep[u] ? off : OffT(0);
     }
@@ -168,29 +193,35 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(const GatherArgs p) {
   }
 }
 
-template <int VB, typename OffT, int BOUNDARY>
+// index arithmetic of a launch: 64-bit offsets, 32-bit, or 32-bit with 24-bit multiplies
+enum class Index { k64, k32, k24 };
+
+template <int VB, typename OffT, int BOUNDARY, bool M24>
 void launch_rank(const GatherArgs& p, uint32_t blocks, hipStream_t s) {
   switch (p.out_rank) {
-    case 2: gather_kernel<VB, 2, OffT, BOUNDARY><<<blocks, kThreads, 0, s>>>(p); break;
-    case 4: gather_kernel<VB, 4, OffT, BOUNDARY><<<blocks, kThreads, 0, s>>>(p); break;
-    case 6: gather_kernel<VB, 6, OffT, BOUNDARY><<<blocks, kThreads, 0, s>>>(p); break;
-    default: gather_kernel<VB, 8, OffT, BOUNDARY><<<blocks, kThreads, 0, s>>>(p); break;
+    case 2: gather_kernel<VB, 2, OffT, BOUNDARY, M24><<<blocks, kThreads, 0, s>>>(p); break;
+    case 4: gather_kernel<VB, 4, OffT, BOUNDARY, M24><<<blocks, kThreads, 0, s>>>(p); break;
+    case 6: gather_kernel<VB, 6, OffT, BOUNDARY, M24><<<blocks, kThreads, 0, s>>>(p); break;
+    default: gather_kernel<VB, 8, OffT, BOUNDARY, M24><<<blocks, kThreads, 0, s>>>(p); break;
   }
 }
 
-template <int VB, typename OffT>
-void launch_off(const GatherArgs& p, int boundary, uint32_t blocks, hipStream_t s) {
-  switch (boundary) {
-    case ES_BOUNDARY_REPLICATE: launch_rank<VB, OffT, ES_BOUNDARY_REPLICATE>(p, blocks, s); break;
-    case ES_BOUNDARY_PERIODIC: launch_rank<VB, OffT, ES_BOUNDARY_PERIODIC>(p, blocks, s); break;
-    default: launch_rank<VB, OffT, ES_BOUNDARY_CONSTANT>(p, blocks, s); break;
+template <int VB, int BOUNDARY>
+void launch_index(const GatherArgs& p, Index index, uint32_t blocks, hipStream_t s) {
+  switch (index) {
+    case Index::k64: launch_rank<VB, int64_t, BOUNDARY, false>(p, blocks, s); break;
+    case Index::k32: launch_rank<VB, int32_t, BOUNDARY, false>(p, blocks, s); break;
+    default: launch_rank<VB, int32_t, BOUNDARY, true>(p, blocks, s); break;
   }
 }
 
 template <int VB>
-void launch_vb(const GatherArgs& p, bool off32, int boundary, uint32_t blocks, hipStream_t s) {
-  if (off32) launch_off<VB, int32_t>(p, boundary, blocks, s);
-  else launch_off<VB, int64_t>(p, boundary, blocks, s);
+void launch_vb(const GatherArgs& p, Index index, int boundary, uint32_t blocks, hipStream_t s) {
+  switch (boundary) {
+    case ES_BOUNDARY_REPLICATE: launch_index<VB, ES_BOUNDARY_REPLICATE>(p, index, blocks, s); break;
+    case ES_BOUNDARY_PERIODIC: launch_index<VB, ES_BOUNDARY_PERIODIC>(p, index, blocks, s); break;
+    default: launch_index<VB, ES_BOUNDARY_CONSTANT>(p, index, blocks, s); break;
+  }
 }
 
 // ---- transposes -----------------------------------------------------------------
@@ -363,6 +394,402 @@ bool try_transpose(const es_gather_desc* d, const void* x, void* out, hipStream_
   return true;
 }
 
+// ---- windows staged through LDS ---------------------------------------------------
+// A window re-reads each input element once per window position (9 times for a
+// 3x3 window); through the vector memory path each re-read costs as much as a
+// fresh load.  When some input dim is windowed, the output is cut into blocks that
+// fix every output dim before a split dim D, take a tile of T coordinates of D and
+// all of every dim after it.  A block's output is then one contiguous chunk, and
+// the input it reads is a box: per input dim, the range of o[pos] + o[win] + offset
+// over the block.  The block loads the box into LDS once, applying the boundary
+// rule on the way (LDS holds the padded input), then writes its chunk from LDS:
+// the output pass has no range checks, and its LDS address depends only on the
+// dims that vary inside the block, lds = sum_{d >= D} (o[d] - first[d]) * lstride[d].
+constexpr int64_t kBoxBudget = 32 * 1024;  // LDS bytes per block
+constexpr int64_t kChunkMax = 64 * 1024;   // output bytes per block
+
+struct TileArgs {
+  const unsigned char* x;
+  unsigned char* out;
+  uint64_t fill;
+  uint32_t blocks;    // real blocks (the grid is padded to whole runs of kRun per XCD)
+  uint32_t out_vecs;  // output vectors per block
+  uint32_t box_vecs;  // vectors in the LDS box
+  int32_t nfix;       // block coordinates: k = 0 the tile index of D, then dims D-1, D-2, ...
+  int32_t nloc;       // dims varying inside a block, innermost first (k = 0 in vectors)
+  int32_t nbox;       // box dims of extent > 1, innermost (in LDS) first (k = 0 in vectors)
+  int32_t nall;       // nbox plus the box dims of extent 1 (stored after them)
+  int32_t tile;       // T
+  int32_t box_shift0; // log2 of the elements per vector along box dim 0
+  uint64_t src_limit; // largest input byte offset a vector may start at
+  FastDiv fix_div[kMax];
+  FastDiv loc_div[kMax];
+  uint32_t loc_lds[kMax];  // LDS bytes per unit of local coordinate k
+  FastDiv box_div[kMax];
+  // box dim k: input coordinate lo_k + r (r the coordinate inside the box), where
+  // lo_k = box_off[k] + sum_f (fixc[f] & box_feed[k][f]), fixc[0] = tile index * T
+  int32_t box_off[kMax];
+  int32_t box_feed[kMax][kMax];
+  int32_t box_chk[kMax];    // the boundary rule applies
+  int32_t box_size[kMax];   // input extent
+  uint32_t box_bias[kMax];  // periodic: a multiple of the extent making coordinates >= 0
+  FastDiv box_wrap[kMax];   // periodic: division by the extent
+  int64_t box_stride[kMax]; // input bytes per unit of coordinate
+};
+
+// Input coordinate c of a box dim under the boundary rule: the byte offset it adds,
+// or `outside` for a constant-boundary coordinate outside the input.
+template <typename UOff, int BOUNDARY>
+__device__ __forceinline__ UOff box_term(const TileArgs& p, int k, int32_t c, bool& outside) {
+  if (p.box_chk[k]) {
+    const int32_t n = p.box_size[k];
+    if constexpr (BOUNDARY == ES_BOUNDARY_CONSTANT) {
+      outside = outside || uint32_t(c) >= uint32_t(n);
+    } else if constexpr (BOUNDARY == ES_BOUNDARY_REPLICATE) {
+      c = min(max(c, 0), n - 1);
+    } else {
+      uint32_t r;
+      p.box_wrap[k].divmod(uint32_t(c) + p.box_bias[k], r);
+      c = int32_t(r);
+    }
+  }
+  return UOff(int64_t(c)) * UOff(p.box_stride[k]);
+}
+
+template <int VB, typename OffT, int BOUNDARY>
+__global__ __launch_bounds__(kThreads) void window_tile_kernel(const TileArgs p) {
+  using V = typename Vec<VB>::type;
+  using UOff = typename std::make_unsigned<OffT>::type;
+  extern __shared__ __align__(16) unsigned char box[];
+  // runs of kRun consecutive blocks per XCD: neighbouring tiles share input rows
+  uint32_t blk = blockIdx.x;
+  if (gridDim.x % (8 * kRun) == 0) {
+    const uint32_t xcd = blk % 8, i = blk / 8;
+    blk = (i / kRun) * 8 * kRun + xcd * kRun + i % kRun;
+  }
+  if (blk >= p.blocks) return;
+
+  int32_t fixc[kMax];
+  {
+    uint32_t rem = blk;
+#pragma unroll
+    for (int f = 0; f < kMax; ++f) {
+      fixc[f] = 0;
+      if (f < p.nfix) {
+        uint32_t r;
+        rem = p.fix_div[f].divmod(rem, r);
+        fixc[f] = int32_t(r);
+      }
+    }
+    fixc[0] *= p.tile;
+  }
+  int32_t lo[kMax];
+#pragma unroll
+  for (int k = 0; k < kMax; ++k) {
+    lo[k] = p.box_off[k];
+#pragma unroll
+    for (int f = 0; f < kMax; ++f) lo[k] += fixc[f] & p.box_feed[k][f];
+  }
+  // box dims of extent 1: one coordinate for the whole block
+  UOff base = 0;
+  bool block_outside = false;
+#pragma unroll
+  for (int k = 0; k < kMax; ++k)
+    if (k >= p.nbox && k < p.nall) base += box_term<UOff, BOUNDARY>(p, k, lo[k], block_outside);
+
+  // 1. the box into LDS (dense, box dim 0 innermost)
+  const V fillv = fill_vec<VB>(p.fill);
+  for (uint32_t first = 0; first < p.box_vecs; first += kUnroll * kThreads) {
+    UOff src[kUnroll];
+    bool keep[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t i = first + u * kThreads + threadIdx.x;
+      const bool valid = i < p.box_vecs;
+      uint32_t rem = valid ? i : 0u;
+      UOff a = base;
+      bool outside = block_outside;
+#pragma unroll
+      for (int k = 0; k < kMax; ++k) {
+        if (k < p.nbox) {
+          uint32_t r = rem;
+          if (k + 1 < p.nbox) {
+            const uint32_t q = div31(p.box_div[k], rem);
+            r = uint32_t(__mul24(int32_t(q), -int32_t(p.box_div[k].d)) + int32_t(rem));
+            rem = q;
+          }
+          const int32_t c = lo[k] + int32_t(k == 0 ? r << p.box_shift0 : r);
+          a += box_term<UOff, BOUNDARY>(p, k, c, outside);
+        }
+      }
+      // (every in-range vector starts at or below src_limit: the compare only
+      // guards the load)
+      keep[u] = valid && !outside && uint64_t(a) <= p.src_limit;
+      src[u] = keep[u] ? a : UOff(0);
+    }
+    V value[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) value[u] = *reinterpret_cast<const V*>(p.x + OffT(src[u]));
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t i = first + u * kThreads + threadIdx.x;
+      if (i < p.box_vecs) reinterpret_cast<V*>(box)[i] = select_vec(keep[u], value[u], fillv);
+    }
+  }
+  __syncthreads();
+
+  // 2. the block's output chunk from LDS
+  V* out = reinterpret_cast<V*>(p.out) + uint64_t(blk) * p.out_vecs;
+  for (uint32_t first = 0; first < p.out_vecs; first += kUnroll * kThreads) {
+    uint32_t off[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t i = first + u * kThreads + threadIdx.x;
+      uint32_t rem = i < p.out_vecs ? i : 0u;
+      uint32_t o = 0;
+#pragma unroll
+      for (int k = 0; k < kMax; ++k) {
+        if (k < p.nloc) {
+          uint32_t r = rem;
+          if (k + 1 < p.nloc) {
+            const uint32_t q = div31(p.loc_div[k], rem);
+            r = uint32_t(__mul24(int32_t(q), -int32_t(p.loc_div[k].d)) + int32_t(rem));
+            rem = q;
+          }
+          o += __umul24(r, p.loc_lds[k]);
+        }
+      }
+      off[u] = o;
+    }
+    V value[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) value[u] = *reinterpret_cast<const V*>(box + off[u]);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t i = first + u * kThreads + threadIdx.x;
+      if (i < p.out_vecs) out[i] = value[u];
+    }
+  }
+}
+
+template <typename OffT, int BOUNDARY>
+void launch_tile_vb(const TileArgs& a, int vb, uint32_t grid, size_t lds, hipStream_t s) {
+  switch (vb) {
+    case 16: window_tile_kernel<16, OffT, BOUNDARY><<<grid, kThreads, lds, s>>>(a); break;
+    case 8: window_tile_kernel<8, OffT, BOUNDARY><<<grid, kThreads, lds, s>>>(a); break;
+    case 4: window_tile_kernel<4, OffT, BOUNDARY><<<grid, kThreads, lds, s>>>(a); break;
+    case 2: window_tile_kernel<2, OffT, BOUNDARY><<<grid, kThreads, lds, s>>>(a); break;
+    default: window_tile_kernel<1, OffT, BOUNDARY><<<grid, kThreads, lds, s>>>(a); break;
+  }
+}
+
+template <typename OffT>
+void launch_tile(const TileArgs& a, int boundary, int vb, uint32_t grid, size_t lds, hipStream_t s) {
+  switch (boundary) {
+    case ES_BOUNDARY_REPLICATE: launch_tile_vb<OffT, ES_BOUNDARY_REPLICATE>(a, vb, grid, lds, s); break;
+    case ES_BOUNDARY_PERIODIC: launch_tile_vb<OffT, ES_BOUNDARY_PERIODIC>(a, vb, grid, lds, s); break;
+    default: launch_tile_vb<OffT, ES_BOUNDARY_CONSTANT>(a, vb, grid, lds, s); break;
+  }
+}
+
+// Output dims d > D span [0, size); d == D spans a tile of T; d < D is fixed.
+inline int64_t tile_span(const es_gather_desc* d, int dim, int split, int64_t t) {
+  if (dim < 0) return 0;
+  if (dim > split) return d->out_size[dim] - 1;
+  return dim == split ? t - 1 : 0;
+}
+
+struct TilePlan {
+  TileArgs a;
+  uint32_t grid;
+  size_t lds;  // bytes of LDS per block
+  bool off32;
+};
+
+// Plan the LDS-staged path for a windowed descriptor, or false when no split saves
+// enough re-reads.  vb: the vector bytes es_gather chose (when wider than an
+// element, the output's innermost dim is fed with unit stride by one input dim).
+bool plan_window_tile(const es_gather_desc* d, const void* x, void* out, int vb, const bool* checked,
+                      uint64_t fill, TilePlan& plan) {
+  const int es_ = d->elem_size, rank = d->out_rank, scale = vb / es_;
+  bool windowed = false;
+  for (int j = 0; j < d->in_rank; ++j) {
+    windowed = windowed || d->win[j] >= 0;
+    if (d->in_size[j] == 0 || d->in_stride[j] < 0) return false;
+  }
+  if (!windowed || x == nullptr) return false;
+
+  // the split (D, T) with the most output bytes per box byte
+  int best_d = -1;
+  int64_t best_t = 0, best_chunk = 0, best_box = 0;
+  for (int split = 0; split < rank; ++split) {
+    int64_t inner = 1;
+    for (int i = split + 1; i < rank; ++i) inner *= d->out_size[i];
+    const int64_t size = d->out_size[split];
+    for (int64_t t = 1; t <= size && t <= 4096; ++t) {
+      if (size % t != 0) continue;
+      if (split == rank - 1 && t % scale != 0) continue;
+      const int64_t chunk = t * inner * es_;
+      if (chunk > kChunkMax) break;
+      int64_t elems = 1;
+      for (int j = 0; j < d->in_rank && elems * es_ <= kBoxBudget; ++j)
+        elems *= 1 + tile_span(d, d->pos[j], split, t) + tile_span(d, d->win[j], split, t);
+      const int64_t bytes = elems * es_;
+      if (bytes > kBoxBudget) continue;
+      // compare chunk / bytes without division; ties go to the larger chunk
+      if (best_d < 0 || chunk * best_box > best_chunk * bytes ||
+          (chunk * best_box == best_chunk * bytes && chunk > best_chunk)) {
+        best_d = split;
+        best_t = t;
+        best_chunk = chunk;
+        best_box = bytes;
+      }
+    }
+  }
+  // at least 1.5 output bytes per box byte, or the staging does not pay
+  if (best_d < 0 || 2 * best_chunk < 3 * best_box) return false;
+  const int split = best_d;
+  const int64_t t = best_t;
+
+  TileArgs& a = plan.a;
+  a.x = static_cast<const unsigned char*>(x);
+  a.out = static_cast<unsigned char*>(out);
+  a.fill = fill;
+  a.tile = int32_t(t);
+  uint64_t total = 1;
+  for (int i = 0; i < rank; ++i) total *= uint64_t(d->out_size[i]);
+  const uint64_t per_block = uint64_t(best_chunk / es_);
+  if (total / per_block > kU32Max) return false;
+  a.blocks = uint32_t(total / per_block);
+  a.out_vecs = uint32_t(per_block / scale);
+
+  // block coordinates: the tile index of D, then the dims before it (extent-1 dims dropped)
+  int fix_dim[kMax];
+  a.nfix = 0;
+  fix_dim[a.nfix] = split;
+  a.fix_div[a.nfix++].init(uint32_t(d->out_size[split] / t));
+  for (int i = split - 1; i >= 0; --i) {
+    if (d->out_size[i] == 1) continue;
+    fix_dim[a.nfix] = i;
+    a.fix_div[a.nfix++].init(uint32_t(d->out_size[i]));
+  }
+  for (int f = a.nfix; f < kMax; ++f) a.fix_div[f].init(1);
+
+  // box dims: extent > 1 first, innermost = the input dim feeding the output's
+  // innermost dim when vectors are wider than an element, else the smallest stride
+  int order[kMax];
+  int64_t ext[kMax];
+  int n_wide = 0;
+  for (int j = 0; j < d->in_rank; ++j) {
+    ext[j] = 1 + tile_span(d, d->pos[j], split, t) + tile_span(d, d->win[j], split, t);
+    if (ext[j] > 1) order[n_wide++] = j;
+  }
+  int first = -1;
+  for (int k = 0; k < n_wide; ++k) {
+    const int j = order[k];
+    const bool feeds_inner = d->pos[j] == rank - 1;
+    if (scale > 1 ? feeds_inner : (first < 0 || d->in_stride[j] < d->in_stride[order[first]])) first = k;
+  }
+  if (scale > 1 && first < 0) return false;
+  if (first > 0) std::swap(order[0], order[first]);
+  // the rest by increasing stride (a short insertion sort)
+  for (int k = 2; k < n_wide; ++k)
+    for (int m = k; m > 1 && d->in_stride[order[m]] < d->in_stride[order[m - 1]]; --m) std::swap(order[m], order[m - 1]);
+  int n_all = n_wide;
+  for (int j = 0; j < d->in_rank; ++j)
+    if (ext[j] == 1) order[n_all++] = j;
+  a.nbox = n_wide;
+  a.nall = n_all;
+  a.box_shift0 = 0;
+  while ((1 << a.box_shift0) < scale) ++a.box_shift0;
+
+  int64_t lds_stride[kMax];  // elements
+  int64_t box_elems = 1;
+  for (int k = 0; k < kMax; ++k) {
+    for (int f = 0; f < kMax; ++f) a.box_feed[k][f] = 0;
+    a.box_off[k] = 0;
+    a.box_chk[k] = 0;
+    a.box_size[k] = 1;
+    a.box_bias[k] = 0;
+    a.box_wrap[k].init(1);
+    a.box_stride[k] = 0;
+    a.box_div[k].init(1);
+    lds_stride[k] = 0;
+    if (k >= n_all) continue;
+    const int j = order[k];
+    if (k < n_wide) {
+      lds_stride[k] = box_elems;
+      box_elems *= ext[j];
+      a.box_div[k].init(uint32_t(k == 0 ? ext[j] / scale : ext[j]));
+    }
+    for (int f = 0; f < a.nfix; ++f)
+      if (d->pos[j] == fix_dim[f] || d->win[j] == fix_dim[f]) a.box_feed[k][f] = -1;
+    a.box_off[k] = int32_t(d->offset[j]);
+    a.box_chk[k] = checked[j] ? 1 : 0;
+    a.box_size[k] = int32_t(d->in_size[j]);
+    const int64_t n = d->in_size[j];
+    const int64_t lowest = d->offset[j] < 0 ? -d->offset[j] : 0;
+    a.box_bias[k] = uint32_t(((lowest + n - 1) / n) * n);
+    a.box_wrap[k].init(uint32_t(n));
+    a.box_stride[k] = d->in_stride[j] * es_;
+  }
+  if (scale > 1 && box_elems % scale != 0) return false;
+  a.box_vecs = uint32_t(box_elems / scale);
+
+  // dims varying inside a block, innermost first; LDS bytes per unit of each
+  a.nloc = 0;
+  for (int i = rank - 1; i >= split; --i) {
+    const int64_t extent = i == split ? t : d->out_size[i];
+    if (extent == 1 && i != rank - 1) continue;
+    int64_t lds = 0;
+    for (int k = 0; k < n_wide; ++k)
+      if (d->pos[order[k]] == i || d->win[order[k]] == i) lds += lds_stride[k];
+    lds *= es_;
+    if (i == rank - 1) lds *= scale;
+    a.loc_div[a.nloc].init(uint32_t(i == rank - 1 ? extent / scale : extent));
+    a.loc_lds[a.nloc++] = uint32_t(lds);
+  }
+  for (int k = a.nloc; k < kMax; ++k) {
+    a.loc_div[k].init(1);
+    a.loc_lds[k] = 0;
+  }
+
+  // 32-bit input offsets when every in-range offset fits in 31 bits
+  int64_t reach = 0;
+  for (int j = 0; j < d->in_rank; ++j) reach += (d->in_size[j] - 1) * d->in_stride[j] * es_;
+  plan.off32 = reach <= 0x3fffffffLL;
+  a.src_limit = uint64_t(reach - (vb - es_) > 0 ? reach - (vb - es_) : 0);
+  // every box coordinate (offset + o[pos] + o[win]) fits comfortably in 31 bits
+  for (int j = 0; j < d->in_rank; ++j) {
+    const int64_t far = d->out_size[d->pos[j]] + (d->win[j] >= 0 ? d->out_size[d->win[j]] : 0) +
+                        (d->offset[j] < 0 ? -d->offset[j] : d->offset[j]);
+    if (far > 0x3fffffffLL) return false;
+  }
+
+  uint64_t grid = a.blocks;
+  if (grid >= 8 * kRun) grid = (grid + 8 * kRun - 1) / (8 * kRun) * (8 * kRun);
+  if (grid > kU32Max) return false;
+  plan.grid = uint32_t(grid);
+  plan.lds = size_t(a.box_vecs) * size_t(vb);
+  // the output pass reads LDS below sum_k (extent_k - 1) * loc_lds[k] + vb
+  uint64_t last = 0;
+  for (int k = 0; k < a.nloc; ++k) last += uint64_t(a.loc_div[k].d - 1) * a.loc_lds[k];
+  if (last + uint64_t(vb) > plan.lds) return false;
+  return true;
+}
+
+// The LDS-staged path of es_gather, or false when plan_window_tile declines.
+bool try_window_tile(const es_gather_desc* d, const void* x, void* out, int vb, const bool* checked,
+                     uint64_t fill, hipStream_t s, int& status) {
+  TilePlan plan;
+  if (!plan_window_tile(d, x, out, vb, checked, fill, plan)) return false;
+  if (plan.off32) launch_tile<int32_t>(plan.a, d->boundary, vb, plan.grid, plan.lds, s);
+  else launch_tile<int64_t>(plan.a, d->boundary, vb, plan.grid, plan.lds, s);
+  set_kernel("gather_window_tile");
+  status = check_launch("es_gather");
+  return true;
+}
+
 }  // namespace
 }  // namespace es
 
@@ -456,8 +883,10 @@ extern "C" int es_gather(const es_gather_desc* d, const void* x, void* out, void
   const int rank = d->out_rank <= 2 ? 2 : (d->out_rank <= 4 ? 4 : (d->out_rank <= 6 ? 6 : 8));
   const int pad = rank - d->out_rank;
   p.out_rank = rank;
-  p.inner_scale = vb / es_;
-  const uint64_t total_vec = total / uint64_t(p.inner_scale);
+  const int inner_scale = vb / es_;  // a power of two
+  p.inner_shift = 0;
+  while ((1 << p.inner_shift) < inner_scale) ++p.inner_shift;
+  const uint64_t total_vec = total / uint64_t(inner_scale);
   if (total_vec > kU32Max) return fail(ES_ERR_UNSUPPORTED, "es_gather: output too large (>2^32 vectors)");
   p.total = uint32_t(total_vec);
   p.base = 0;
@@ -466,7 +895,7 @@ extern "C" int es_gather(const es_gather_desc* d, const void* x, void* out, void
     const int src_dim = i - pad;  // descriptor dim behind padded dim i
     if (i < rank && src_dim >= 0) {
       int64_t sz = d->out_size[src_dim];
-      if (src_dim == inner) sz /= p.inner_scale;
+      if (src_dim == inner) sz /= inner_scale;
       p.out_div[i].init(uint32_t(sz));
     } else {
       p.out_div[i].init(1);
@@ -506,6 +935,9 @@ extern "C" int es_gather(const es_gather_desc* d, const void* x, void* out, void
   }
   p.nchk = nchk;
 
+  // the innermost dim steps by whole vectors
+  p.out_stride[rank - 1] *= inner_scale;
+
   // 32-bit source offsets when every in-range offset (and each term of it) fits in 31 bits
   bool off32 = true;
   {
@@ -519,18 +951,43 @@ extern "C" int es_gather(const es_gather_desc* d, const void* x, void* out, void
       if (p.out_stride[i] > 0x7fffffffLL || p.out_stride[i] < 0) off32 = false;
     if (reach > 0x3fffffffLL || p.base < -0x3fffffffLL || p.base > 0x3fffffffLL) off32 = false;
   }
+  // 24-bit multiplies: fewer than 2^31 vectors, sizes and quotients below 2^23
+  // (v_mad_i32_i24 takes them signed), byte strides below 2^24
+  Index index = off32 ? Index::k32 : Index::k64;
+  if (off32 && total_vec < 0x80000000ull) {
+    bool m24 = total_vec / p.out_div[rank - 1].d < (1u << 23);
+    for (int i = 0; i < rank; ++i) {
+      if (p.out_div[i].d >= (1u << 23)) m24 = false;
+      if (p.out_stride[i] >= (1 << 24)) m24 = false;
+    }
+    if (m24) index = Index::k24;
+  }
   const uint64_t per_group = uint64_t(kUnroll) * kThreads;
   uint64_t blocks64 = (total_vec + per_group - 1) / per_group;
   // whole runs of kRun work-groups per XCD (the extra groups find no work)
   if (blocks64 >= 8 * kRun) blocks64 = (blocks64 + 8 * kRun - 1) / (8 * kRun) * (8 * kRun);
   const uint32_t blocks = uint32_t(blocks64 > 1048576 ? 1048576 : blocks64);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (vb) {
-    case 16: launch_vb<16>(p, off32, d->boundary, blocks, s); set_kernel("gather_v16"); break;
-    case 8: launch_vb<8>(p, off32, d->boundary, blocks, s); set_kernel("gather_v8"); break;
-    case 4: launch_vb<4>(p, off32, d->boundary, blocks, s); set_kernel("gather_v4"); break;
-    case 2: launch_vb<2>(p, off32, d->boundary, blocks, s); set_kernel("gather_v2"); break;
-    default: launch_vb<1>(p, off32, d->boundary, blocks, s); set_kernel("gather_v1"); break;
+  {
+    int status = ES_OK;
+    if (try_window_tile(d, x, out, vb, checked, p.fill, s, status)) return status;
   }
+
+  // kernel names: vector bytes, then the index arithmetic (none = 32-bit)
+  static const char* const kNames[5][3] = {{"gather_v1_o64", "gather_v1", "gather_v1_m24"},
+                                           {"gather_v2_o64", "gather_v2", "gather_v2_m24"},
+                                           {"gather_v4_o64", "gather_v4", "gather_v4_m24"},
+                                           {"gather_v8_o64", "gather_v8", "gather_v8_m24"},
+                                           {"gather_v16_o64", "gather_v16", "gather_v16_m24"}};
+  int vb_log = 0;
+  while ((1 << vb_log) < vb) ++vb_log;
+  switch (vb) {
+    case 16: launch_vb<16>(p, index, d->boundary, blocks, s); break;
+    case 8: launch_vb<8>(p, index, d->boundary, blocks, s); break;
+    case 4: launch_vb<4>(p, index, d->boundary, blocks, s); break;
+    case 2: launch_vb<2>(p, index, d->boundary, blocks, s); break;
+    default: launch_vb<1>(p, index, d->boundary, blocks, s); break;
+  }
+  set_kernel(kNames[vb_log][int(index)]);
   return check_launch("es_gather");
 }
