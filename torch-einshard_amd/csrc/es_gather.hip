@@ -401,65 +401,93 @@ bool try_transpose(const es_gather_desc* d, const void* x, void* out, hipStream_
 // fix every output dim before a split dim D, take a tile of T coordinates of D and
 // all of every dim after it.  A block's output is then one contiguous chunk, and
 // the input it reads is a box: per input dim, the range of o[pos] + o[win] + offset
-// over the block.  The block loads the box into LDS once, applying the boundary
-// rule on the way (LDS holds the padded input), then writes its chunk from LDS:
-// the output pass has no range checks, and its LDS address depends only on the
-// dims that vary inside the block, lds = sum_{d >= D} (o[d] - first[d]) * lstride[d].
+// over the block.  A work-group loads its block's box into LDS once, applying the
+// boundary rule on the way (LDS holds the padded input), then writes the chunk
+// from LDS: the output pass has no range checks, and its LDS address depends only
+// on the dims that vary inside the block, lds = sum_{d >= D} (o[d] - first[d]) *
+// lstride[d].  One block per work-group: a work-group that went on to a second
+// block would wait for its first block's stores (the vector memory counter
+// counts stores too) before it could use the second box's loads.
+//
+// Inside a block every index stays below 2^15, so divisions take one full-rate
+// 24-bit multiply (SmallDiv) and addresses 24-bit multiply-adds.
 constexpr int64_t kBoxBudget = 32 * 1024;  // LDS bytes per block
 constexpr int64_t kChunkMax = 64 * 1024;   // output bytes per block
+constexpr int kTileDims = 4;               // box dims of extent > 1; dims varying in a block
+constexpr uint32_t kSmallBits = 15;        // block-local indices stay below 2^15
+
+// q = n / d for n < 2^kSmallBits: q = (n * m) >> s with s = kSmallBits + ceil(log2 d)
+// and m = ceil(2^s / d).  The error n (m d - 2^s) / (d 2^s) < 2^kSmallBits / 2^s <= 1/d
+// keeps the floor exact; m <= 2^(kSmallBits + 1), so n * m < 2^32.
+struct SmallDiv {
+  uint32_t d, m, s;
+  __host__ void init(uint32_t divisor) {
+    d = divisor < 1 ? 1 : divisor;
+    uint32_t l = 0;
+    while ((1u << l) < d) ++l;
+    s = kSmallBits + l;
+    m = uint32_t(((uint64_t(1) << s) + d - 1) / d);
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const { return __umul24(n, m) >> s; }
+};
 
 struct TileArgs {
   const unsigned char* x;
   unsigned char* out;
   uint64_t fill;
-  uint32_t blocks;    // real blocks (the grid is padded to whole runs of kRun per XCD)
-  uint32_t out_vecs;  // output vectors per block
-  uint32_t box_vecs;  // vectors in the LDS box
-  int32_t nfix;       // block coordinates: k = 0 the tile index of D, then dims D-1, D-2, ...
-  int32_t nloc;       // dims varying inside a block, innermost first (k = 0 in vectors)
-  int32_t nbox;       // box dims of extent > 1, innermost (in LDS) first (k = 0 in vectors)
-  int32_t nall;       // nbox plus the box dims of extent 1 (stored after them)
-  int32_t tile;       // T
-  int32_t box_shift0; // log2 of the elements per vector along box dim 0
-  uint64_t src_limit; // largest input byte offset a vector may start at
+  uint32_t blocks;     // real blocks (the grid is padded to whole runs of kRun per XCD)
+  uint32_t out_vecs;   // output vectors per block
+  uint32_t box_vecs;   // vectors in the LDS box
+  uint32_t src_limit;  // largest input byte offset a vector may start at
+  int32_t nfix;        // block coordinates: k = 0 the tile index of D, then dims D-1, D-2, ...
+  int32_t tile;        // T
+  int32_t box_shift0;  // log2 of the elements per vector along box dim 0
+  int32_t ncon;        // input dims of extent 1 in the box (one coordinate per block)
   FastDiv fix_div[kMax];
-  FastDiv loc_div[kMax];
-  uint32_t loc_lds[kMax];  // LDS bytes per unit of local coordinate k
-  FastDiv box_div[kMax];
-  // box dim k: input coordinate lo_k + r (r the coordinate inside the box), where
-  // lo_k = box_off[k] + sum_f (fixc[f] & box_feed[k][f]), fixc[0] = tile index * T
-  int32_t box_off[kMax];
-  int32_t box_feed[kMax][kMax];
-  int32_t box_chk[kMax];    // the boundary rule applies
-  int32_t box_size[kMax];   // input extent
-  uint32_t box_bias[kMax];  // periodic: a multiple of the extent making coordinates >= 0
-  FastDiv box_wrap[kMax];   // periodic: division by the extent
-  int64_t box_stride[kMax]; // input bytes per unit of coordinate
+  // dims varying inside a block, innermost first (k = 0 counts vectors), merged where
+  // contiguous in LDS; the unused ones have extent 1
+  SmallDiv loc_div[kTileDims];
+  uint32_t loc_lds[kTileDims];  // LDS bytes per unit of coordinate
+  // box dims, innermost (in LDS) first, k = 0 counting vectors; the unused ones have
+  // extent 1.  Input coordinate lo_k + r, lo_k = box_off[k] + sum_f (fixc[f] &
+  // box_feed[k][f]) with fixc[0] = tile index * T.
+  SmallDiv box_div[kTileDims];
+  int32_t box_off[kTileDims];
+  int32_t box_feed[kTileDims][kMax];
+  int32_t box_size[kTileDims];     // input extent; 2^30 for a dim that never leaves it
+  uint32_t box_bias[kTileDims];    // periodic: a multiple of the extent making coordinates >= 0
+  FastDiv box_wrap[kTileDims];     // periodic: division by the extent
+  int32_t box_chk[kTileDims];      // periodic: the dim can leave its extent
+  int32_t box_stride[kTileDims];   // input bytes per unit of coordinate, below 2^23
+  // input dims of extent 1 in the box, with the same fields
+  int32_t con_off[kMax];
+  int32_t con_feed[kMax][kMax];
+  int32_t con_size[kMax];
+  uint32_t con_bias[kMax];
+  FastDiv con_wrap[kMax];
+  int32_t con_chk[kMax];
+  int32_t con_stride[kMax];
 };
 
-// Input coordinate c of a box dim under the boundary rule: the byte offset it adds,
-// or `outside` for a constant-boundary coordinate outside the input.
-template <typename UOff, int BOUNDARY>
-__device__ __forceinline__ UOff box_term(const TileArgs& p, int k, int32_t c, bool& outside) {
-  if (p.box_chk[k]) {
-    const int32_t n = p.box_size[k];
-    if constexpr (BOUNDARY == ES_BOUNDARY_CONSTANT) {
-      outside = outside || uint32_t(c) >= uint32_t(n);
-    } else if constexpr (BOUNDARY == ES_BOUNDARY_REPLICATE) {
-      c = min(max(c, 0), n - 1);
-    } else {
-      uint32_t r;
-      p.box_wrap[k].divmod(uint32_t(c) + p.box_bias[k], r);
-      c = int32_t(r);
-    }
+// Coordinate c of a box dim under the boundary rule (constant: only `outside` is set).
+template <int BOUNDARY>
+__device__ __forceinline__ int32_t bound_coord(int32_t c, int32_t size, uint32_t bias, const FastDiv& wrap,
+                                               int32_t chk, bool& outside) {
+  if constexpr (BOUNDARY == ES_BOUNDARY_CONSTANT) {
+    outside = outside || uint32_t(c) >= uint32_t(size);
+  } else if constexpr (BOUNDARY == ES_BOUNDARY_REPLICATE) {
+    c = min(max(c, 0), size - 1);
+  } else if (chk) {
+    uint32_t r;
+    wrap.divmod(uint32_t(c) + bias, r);
+    c = int32_t(r);
   }
-  return UOff(int64_t(c)) * UOff(p.box_stride[k]);
+  return c;
 }
 
-template <int VB, typename OffT, int BOUNDARY>
+template <int VB, int BOUNDARY, int NL>
 __global__ __launch_bounds__(kThreads) void window_tile_kernel(const TileArgs p) {
   using V = typename Vec<VB>::type;
-  using UOff = typename std::make_unsigned<OffT>::type;
   extern __shared__ __align__(16) unsigned char box[];
   // runs of kRun consecutive blocks per XCD: neighbouring tiles share input rows
   uint32_t blk = blockIdx.x;
@@ -483,112 +511,114 @@ __global__ __launch_bounds__(kThreads) void window_tile_kernel(const TileArgs p)
     }
     fixc[0] *= p.tile;
   }
-  int32_t lo[kMax];
+  // input dims of extent 1: one coordinate and one address term for the block
+  uint32_t base = 0;
+  bool block_outside = false;
+  for (int k = 0; k < p.ncon; ++k) {
+    int32_t c = p.con_off[k];
 #pragma unroll
-  for (int k = 0; k < kMax; ++k) {
+    for (int f = 0; f < kMax; ++f) c += fixc[f] & p.con_feed[k][f];
+    c = bound_coord<BOUNDARY>(c, p.con_size[k], p.con_bias[k], p.con_wrap[k], p.con_chk[k], block_outside);
+    base += uint32_t(c) * uint32_t(p.con_stride[k]);
+  }
+  int32_t lo[kTileDims];
+#pragma unroll
+  for (int k = 0; k < kTileDims; ++k) {
     lo[k] = p.box_off[k];
 #pragma unroll
     for (int f = 0; f < kMax; ++f) lo[k] += fixc[f] & p.box_feed[k][f];
   }
-  // box dims of extent 1: one coordinate for the whole block
-  UOff base = 0;
-  bool block_outside = false;
-#pragma unroll
-  for (int k = 0; k < kMax; ++k)
-    if (k >= p.nbox && k < p.nall) base += box_term<UOff, BOUNDARY>(p, k, lo[k], block_outside);
 
-  // 1. the box into LDS (dense, box dim 0 innermost)
+  // 1. the box into LDS (dense, box dim 0 innermost).  LDS holds whole groups of
+  // kUnroll * kThreads vectors, so every lane writes its slots unconditionally (the
+  // slots past the box get fill) and the loads stay back to back.
   const V fillv = fill_vec<VB>(p.fill);
   for (uint32_t first = 0; first < p.box_vecs; first += kUnroll * kThreads) {
-    UOff src[kUnroll];
+    uint32_t src[kUnroll];
     bool keep[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint32_t i = first + u * kThreads + threadIdx.x;
       const bool valid = i < p.box_vecs;
-      uint32_t rem = valid ? i : 0u;
-      UOff a = base;
+      uint32_t n = valid ? i : 0u;
+      uint32_t a = base;
       bool outside = block_outside;
 #pragma unroll
-      for (int k = 0; k < kMax; ++k) {
-        if (k < p.nbox) {
-          uint32_t r = rem;
-          if (k + 1 < p.nbox) {
-            const uint32_t q = div31(p.box_div[k], rem);
-            r = uint32_t(__mul24(int32_t(q), -int32_t(p.box_div[k].d)) + int32_t(rem));
-            rem = q;
-          }
-          const int32_t c = lo[k] + int32_t(k == 0 ? r << p.box_shift0 : r);
-          a += box_term<UOff, BOUNDARY>(p, k, c, outside);
+      for (int k = 0; k < kTileDims; ++k) {
+        uint32_t r = n;
+        if (k + 1 < kTileDims) {
+          const uint32_t q = p.box_div[k].div(n);
+          r = n - __umul24(q, p.box_div[k].d);
+          n = q;
         }
+        int32_t c = lo[k] + int32_t(k == 0 ? r << p.box_shift0 : r);
+        c = bound_coord<BOUNDARY>(c, p.box_size[k], p.box_bias[k], p.box_wrap[k], p.box_chk[k], outside);
+        a += uint32_t(__mul24(c, p.box_stride[k]));
       }
-      // (every in-range vector starts at or below src_limit: the compare only
-      // guards the load)
-      keep[u] = valid && !outside && uint64_t(a) <= p.src_limit;
-      src[u] = keep[u] ? a : UOff(0);
+      // every in-range vector starts at or below src_limit: the compare only guards the load
+      keep[u] = valid && !outside && a <= p.src_limit;
+      src[u] = keep[u] ? a : 0u;
     }
     V value[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) value[u] = *reinterpret_cast<const V*>(p.x + OffT(src[u]));
+    for (int u = 0; u < kUnroll; ++u) value[u] = *reinterpret_cast<const V*>(p.x + src[u]);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t i = first + u * kThreads + threadIdx.x;
-      if (i < p.box_vecs) reinterpret_cast<V*>(box)[i] = select_vec(keep[u], value[u], fillv);
-    }
+    for (int u = 0; u < kUnroll; ++u)
+      reinterpret_cast<V*>(box)[first + u * kThreads + threadIdx.x] = select_vec(keep[u], value[u], fillv);
   }
   __syncthreads();
 
-  // 2. the block's output chunk from LDS
+  // 2. the block's output chunk from LDS: whole groups of kUnroll vectors per
+  // thread (all LDS reads issued before the stores), then the rest one at a time
+  auto lds_of = [&](uint32_t n) {
+    uint32_t o = 0;
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      uint32_t r = n;
+      if (k + 1 < NL) {
+        const uint32_t q = p.loc_div[k].div(n);
+        r = n - __umul24(q, p.loc_div[k].d);
+        n = q;
+      }
+      o += __umul24(r, p.loc_lds[k]);
+    }
+    return o;
+  };
   V* out = reinterpret_cast<V*>(p.out) + uint64_t(blk) * p.out_vecs;
-  for (uint32_t first = 0; first < p.out_vecs; first += kUnroll * kThreads) {
+  const uint32_t full = p.out_vecs - p.out_vecs % (kUnroll * kThreads);
+  uint32_t first = 0;
+  for (; first < full; first += kUnroll * kThreads) {
     uint32_t off[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t i = first + u * kThreads + threadIdx.x;
-      uint32_t rem = i < p.out_vecs ? i : 0u;
-      uint32_t o = 0;
-#pragma unroll
-      for (int k = 0; k < kMax; ++k) {
-        if (k < p.nloc) {
-          uint32_t r = rem;
-          if (k + 1 < p.nloc) {
-            const uint32_t q = div31(p.loc_div[k], rem);
-            r = uint32_t(__mul24(int32_t(q), -int32_t(p.loc_div[k].d)) + int32_t(rem));
-            rem = q;
-          }
-          o += __umul24(r, p.loc_lds[k]);
-        }
-      }
-      off[u] = o;
-    }
+    for (int u = 0; u < kUnroll; ++u) off[u] = lds_of(first + u * kThreads + threadIdx.x);
     V value[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) value[u] = *reinterpret_cast<const V*>(box + off[u]);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t i = first + u * kThreads + threadIdx.x;
-      if (i < p.out_vecs) out[i] = value[u];
-    }
+    for (int u = 0; u < kUnroll; ++u) out[first + u * kThreads + threadIdx.x] = value[u];
+  }
+  for (uint32_t i = first + threadIdx.x; i < p.out_vecs; i += kThreads)
+    out[i] = *reinterpret_cast<const V*>(box + lds_of(i));
+}
+
+template <int VB, int BOUNDARY>
+void launch_tile_nl(const TileArgs& a, int nl, uint32_t grid, size_t lds, hipStream_t s) {
+  switch (nl) {
+    case 1: window_tile_kernel<VB, BOUNDARY, 1><<<grid, kThreads, lds, s>>>(a); break;
+    case 2: window_tile_kernel<VB, BOUNDARY, 2><<<grid, kThreads, lds, s>>>(a); break;
+    case 3: window_tile_kernel<VB, BOUNDARY, 3><<<grid, kThreads, lds, s>>>(a); break;
+    default: window_tile_kernel<VB, BOUNDARY, 4><<<grid, kThreads, lds, s>>>(a); break;
   }
 }
 
-template <typename OffT, int BOUNDARY>
-void launch_tile_vb(const TileArgs& a, int vb, uint32_t grid, size_t lds, hipStream_t s) {
+template <int BOUNDARY>
+void launch_tile_vb(const TileArgs& a, int vb, int nl, uint32_t grid, size_t lds, hipStream_t s) {
   switch (vb) {
-    case 16: window_tile_kernel<16, OffT, BOUNDARY><<<grid, kThreads, lds, s>>>(a); break;
-    case 8: window_tile_kernel<8, OffT, BOUNDARY><<<grid, kThreads, lds, s>>>(a); break;
-    case 4: window_tile_kernel<4, OffT, BOUNDARY><<<grid, kThreads, lds, s>>>(a); break;
-    case 2: window_tile_kernel<2, OffT, BOUNDARY><<<grid, kThreads, lds, s>>>(a); break;
-    default: window_tile_kernel<1, OffT, BOUNDARY><<<grid, kThreads, lds, s>>>(a); break;
-  }
-}
-
-template <typename OffT>
-void launch_tile(const TileArgs& a, int boundary, int vb, uint32_t grid, size_t lds, hipStream_t s) {
-  switch (boundary) {
-    case ES_BOUNDARY_REPLICATE: launch_tile_vb<OffT, ES_BOUNDARY_REPLICATE>(a, vb, grid, lds, s); break;
-    case ES_BOUNDARY_PERIODIC: launch_tile_vb<OffT, ES_BOUNDARY_PERIODIC>(a, vb, grid, lds, s); break;
-    default: launch_tile_vb<OffT, ES_BOUNDARY_CONSTANT>(a, vb, grid, lds, s); break;
+    case 16: launch_tile_nl<16, BOUNDARY>(a, nl, grid, lds, s); break;
+    case 8: launch_tile_nl<8, BOUNDARY>(a, nl, grid, lds, s); break;
+    case 4: launch_tile_nl<4, BOUNDARY>(a, nl, grid, lds, s); break;
+    case 2: launch_tile_nl<2, BOUNDARY>(a, nl, grid, lds, s); break;
+    default: launch_tile_nl<1, BOUNDARY>(a, nl, grid, lds, s); break;
   }
 }
 
@@ -599,27 +629,103 @@ inline int64_t tile_span(const es_gather_desc* d, int dim, int split, int64_t t)
   return dim == split ? t - 1 : 0;
 }
 
+// The box and block layout of one split (D, T).
+struct TileLayout {
+  int64_t ext[kMax];        // box extent of each input dim
+  int order[kMax];          // box dims of extent > 1, innermost (in LDS) first
+  int n_wide;
+  int64_t lds_stride[kTileDims];  // elements
+  int64_t box_elems;
+  int64_t loc_ext[kMax];    // dims varying inside a block, innermost first, merged
+  int64_t loc_lds[kMax];    // LDS bytes per unit of their coordinate
+  int nl;
+};
+
+// Box dims of extent > 1: innermost the input dim feeding the output's innermost dim
+// when vectors are wider than an element, else the smallest stride; the rest by
+// increasing stride.  Dims varying inside a block: innermost first, a dim whose LDS
+// step is the inner one's whole extent merged into it.  False when the kernel's
+// fixed dim counts or 24-bit strides do not fit.
+bool tile_layout(const es_gather_desc* d, int split, int64_t t, int scale, TileLayout& L) {
+  const int es_ = d->elem_size, rank = d->out_rank;
+  L.n_wide = 0;
+  for (int j = 0; j < d->in_rank; ++j) {
+    L.ext[j] = 1 + tile_span(d, d->pos[j], split, t) + tile_span(d, d->win[j], split, t);
+    if (L.ext[j] > 1) {
+      if (L.n_wide == kTileDims || d->in_stride[j] * es_ >= (int64_t(1) << 23)) return false;
+      L.order[L.n_wide++] = j;
+    }
+  }
+  int first = -1;
+  for (int k = 0; k < L.n_wide; ++k) {
+    const int j = L.order[k];
+    const bool feeds_inner = d->pos[j] == rank - 1;
+    if (scale > 1 ? feeds_inner : (first < 0 || d->in_stride[j] < d->in_stride[L.order[first]])) first = k;
+  }
+  if (scale > 1 && first < 0) return false;
+  if (first > 0) std::swap(L.order[0], L.order[first]);
+  for (int k = 2; k < L.n_wide; ++k)
+    for (int m = k; m > 1 && d->in_stride[L.order[m]] < d->in_stride[L.order[m - 1]]; --m)
+      std::swap(L.order[m], L.order[m - 1]);
+  L.box_elems = 1;
+  for (int k = 0; k < kTileDims; ++k) {
+    L.lds_stride[k] = k < L.n_wide ? L.box_elems : 0;
+    if (k < L.n_wide) L.box_elems *= L.ext[L.order[k]];
+  }
+  if (scale > 1 && (L.ext[L.order[0]] % scale != 0)) return false;
+  L.nl = 0;
+  for (int i = rank - 1; i >= split; --i) {
+    int64_t extent = i == split ? t : d->out_size[i];
+    if (extent == 1 && i != rank - 1) continue;
+    int64_t lds = 0;
+    for (int k = 0; k < L.n_wide; ++k)
+      if (d->pos[L.order[k]] == i || d->win[L.order[k]] == i) lds += L.lds_stride[k];
+    lds *= es_;
+    if (i == rank - 1) {
+      lds *= scale;
+      extent /= scale;
+    }
+    if (L.nl > 0 && lds == L.loc_lds[L.nl - 1] * L.loc_ext[L.nl - 1]) {
+      L.loc_ext[L.nl - 1] *= extent;
+    } else {
+      L.loc_ext[L.nl] = extent;
+      L.loc_lds[L.nl++] = lds;
+    }
+  }
+  return L.nl <= kTileDims;
+}
+
 struct TilePlan {
   TileArgs a;
   uint32_t grid;
   size_t lds;  // bytes of LDS per block
-  bool off32;
+  int nl;      // dims varying inside a block
 };
 
 // Plan the LDS-staged path for a windowed descriptor, or false when no split saves
-// enough re-reads.  vb: the vector bytes es_gather chose (when wider than an
-// element, the output's innermost dim is fed with unit stride by one input dim).
+// enough re-reads or the block does not fit the kernel's index arithmetic.  vb: the
+// vector bytes es_gather chose (when wider than an element, the output's innermost
+// dim is fed with unit stride by one input dim, never out of range).
 bool plan_window_tile(const es_gather_desc* d, const void* x, void* out, int vb, const bool* checked,
                       uint64_t fill, TilePlan& plan) {
   const int es_ = d->elem_size, rank = d->out_rank, scale = vb / es_;
   bool windowed = false;
+  int64_t reach = 0;
   for (int j = 0; j < d->in_rank; ++j) {
     windowed = windowed || d->win[j] >= 0;
     if (d->in_size[j] == 0 || d->in_stride[j] < 0) return false;
+    reach += (d->in_size[j] - 1) * d->in_stride[j] * es_;
+    // every coordinate, offset + o[pos] + o[win], stays far inside 24 bits
+    const int64_t far = d->out_size[d->pos[j]] + (d->win[j] >= 0 ? d->out_size[d->win[j]] : 0) +
+                        (d->offset[j] < 0 ? -d->offset[j] : d->offset[j]);
+    if (far >= (int64_t(1) << 22)) return false;
   }
-  if (!windowed || x == nullptr) return false;
+  // 32-bit input offsets: every in-range offset fits in 30 bits
+  if (!windowed || x == nullptr || reach > 0x3fffffffLL) return false;
 
   // the split (D, T) with the most output bytes per box byte
+  const int64_t max_vecs = int64_t(1) << kSmallBits;
+  TileLayout L;
   int best_d = -1;
   int64_t best_t = 0, best_chunk = 0, best_box = 0;
   for (int split = 0; split < rank; ++split) {
@@ -630,15 +736,16 @@ bool plan_window_tile(const es_gather_desc* d, const void* x, void* out, int vb,
       if (size % t != 0) continue;
       if (split == rank - 1 && t % scale != 0) continue;
       const int64_t chunk = t * inner * es_;
-      if (chunk > kChunkMax) break;
+      if (chunk > kChunkMax || chunk / vb > max_vecs) break;
       int64_t elems = 1;
       for (int j = 0; j < d->in_rank && elems * es_ <= kBoxBudget; ++j)
         elems *= 1 + tile_span(d, d->pos[j], split, t) + tile_span(d, d->win[j], split, t);
       const int64_t bytes = elems * es_;
-      if (bytes > kBoxBudget) continue;
+      if (bytes > kBoxBudget || bytes / vb > max_vecs) continue;
       // compare chunk / bytes without division; ties go to the larger chunk
-      if (best_d < 0 || chunk * best_box > best_chunk * bytes ||
-          (chunk * best_box == best_chunk * bytes && chunk > best_chunk)) {
+      const bool better = best_d < 0 || chunk * best_box > best_chunk * bytes ||
+                          (chunk * best_box == best_chunk * bytes && chunk > best_chunk);
+      if (better && tile_layout(d, split, t, scale, L)) {
         best_d = split;
         best_t = t;
         best_chunk = chunk;
@@ -662,6 +769,7 @@ bool plan_window_tile(const es_gather_desc* d, const void* x, void* out, int vb,
   if (total / per_block > kU32Max) return false;
   a.blocks = uint32_t(total / per_block);
   a.out_vecs = uint32_t(per_block / scale);
+  a.src_limit = uint32_t(reach - (vb - es_) > 0 ? reach - (vb - es_) : 0);
 
   // block coordinates: the tile index of D, then the dims before it (extent-1 dims dropped)
   int fix_dim[kMax];
@@ -675,106 +783,90 @@ bool plan_window_tile(const es_gather_desc* d, const void* x, void* out, int vb,
   }
   for (int f = a.nfix; f < kMax; ++f) a.fix_div[f].init(1);
 
-  // box dims: extent > 1 first, innermost = the input dim feeding the output's
-  // innermost dim when vectors are wider than an element, else the smallest stride
-  int order[kMax];
-  int64_t ext[kMax];
-  int n_wide = 0;
-  for (int j = 0; j < d->in_rank; ++j) {
-    ext[j] = 1 + tile_span(d, d->pos[j], split, t) + tile_span(d, d->win[j], split, t);
-    if (ext[j] > 1) order[n_wide++] = j;
-  }
-  int first = -1;
-  for (int k = 0; k < n_wide; ++k) {
-    const int j = order[k];
-    const bool feeds_inner = d->pos[j] == rank - 1;
-    if (scale > 1 ? feeds_inner : (first < 0 || d->in_stride[j] < d->in_stride[order[first]])) first = k;
-  }
-  if (scale > 1 && first < 0) return false;
-  if (first > 0) std::swap(order[0], order[first]);
-  // the rest by increasing stride (a short insertion sort)
-  for (int k = 2; k < n_wide; ++k)
-    for (int m = k; m > 1 && d->in_stride[order[m]] < d->in_stride[order[m - 1]]; --m) std::swap(order[m], order[m - 1]);
-  int n_all = n_wide;
-  for (int j = 0; j < d->in_rank; ++j)
-    if (ext[j] == 1) order[n_all++] = j;
-  a.nbox = n_wide;
-  a.nall = n_all;
+  if (!tile_layout(d, split, t, scale, L)) return false;
+  const int n_wide = L.n_wide;
+  const int* order = L.order;
+  const int64_t* ext = L.ext;
   a.box_shift0 = 0;
   while ((1 << a.box_shift0) < scale) ++a.box_shift0;
 
-  int64_t lds_stride[kMax];  // elements
-  int64_t box_elems = 1;
-  for (int k = 0; k < kMax; ++k) {
+  auto periodic_bias = [&](int j) {
+    const int64_t n = d->in_size[j];
+    const int64_t lowest = d->offset[j] < 0 ? -d->offset[j] : 0;
+    return uint32_t(((lowest + n - 1) / n) * n);
+  };
+  for (int k = 0; k < kTileDims; ++k) {
     for (int f = 0; f < kMax; ++f) a.box_feed[k][f] = 0;
     a.box_off[k] = 0;
-    a.box_chk[k] = 0;
-    a.box_size[k] = 1;
+    a.box_size[k] = 1 << 30;
     a.box_bias[k] = 0;
     a.box_wrap[k].init(1);
+    a.box_chk[k] = 0;
     a.box_stride[k] = 0;
     a.box_div[k].init(1);
-    lds_stride[k] = 0;
-    if (k >= n_all) continue;
+    if (k >= n_wide) continue;
     const int j = order[k];
-    if (k < n_wide) {
-      lds_stride[k] = box_elems;
-      box_elems *= ext[j];
-      a.box_div[k].init(uint32_t(k == 0 ? ext[j] / scale : ext[j]));
-    }
+    const int64_t stride = d->in_stride[j] * es_;
+    a.box_div[k].init(uint32_t(k == 0 ? ext[j] / scale : ext[j]));
     for (int f = 0; f < a.nfix; ++f)
       if (d->pos[j] == fix_dim[f] || d->win[j] == fix_dim[f]) a.box_feed[k][f] = -1;
     a.box_off[k] = int32_t(d->offset[j]);
-    a.box_chk[k] = checked[j] ? 1 : 0;
-    a.box_size[k] = int32_t(d->in_size[j]);
-    const int64_t n = d->in_size[j];
-    const int64_t lowest = d->offset[j] < 0 ? -d->offset[j] : 0;
-    a.box_bias[k] = uint32_t(((lowest + n - 1) / n) * n);
-    a.box_wrap[k].init(uint32_t(n));
-    a.box_stride[k] = d->in_stride[j] * es_;
+    if (checked[j]) {
+      a.box_size[k] = int32_t(d->in_size[j]);
+      a.box_bias[k] = periodic_bias(j);
+      a.box_wrap[k].init(uint32_t(d->in_size[j]));
+      a.box_chk[k] = 1;
+    }
+    a.box_stride[k] = int32_t(stride);
   }
-  if (scale > 1 && box_elems % scale != 0) return false;
-  a.box_vecs = uint32_t(box_elems / scale);
+  a.box_vecs = uint32_t(L.box_elems / scale);
 
-  // dims varying inside a block, innermost first; LDS bytes per unit of each
-  a.nloc = 0;
-  for (int i = rank - 1; i >= split; --i) {
-    const int64_t extent = i == split ? t : d->out_size[i];
-    if (extent == 1 && i != rank - 1) continue;
-    int64_t lds = 0;
-    for (int k = 0; k < n_wide; ++k)
-      if (d->pos[order[k]] == i || d->win[order[k]] == i) lds += lds_stride[k];
-    lds *= es_;
-    if (i == rank - 1) lds *= scale;
-    a.loc_div[a.nloc].init(uint32_t(i == rank - 1 ? extent / scale : extent));
-    a.loc_lds[a.nloc++] = uint32_t(lds);
+  // input dims of extent 1
+  a.ncon = 0;
+  for (int k = 0; k < kMax; ++k) {
+    for (int f = 0; f < kMax; ++f) a.con_feed[k][f] = 0;
+    a.con_off[k] = 0;
+    a.con_size[k] = 1 << 30;
+    a.con_bias[k] = 0;
+    a.con_wrap[k].init(1);
+    a.con_chk[k] = 0;
+    a.con_stride[k] = 0;
   }
-  for (int k = a.nloc; k < kMax; ++k) {
-    a.loc_div[k].init(1);
-    a.loc_lds[k] = 0;
-  }
-
-  // 32-bit input offsets when every in-range offset fits in 31 bits
-  int64_t reach = 0;
-  for (int j = 0; j < d->in_rank; ++j) reach += (d->in_size[j] - 1) * d->in_stride[j] * es_;
-  plan.off32 = reach <= 0x3fffffffLL;
-  a.src_limit = uint64_t(reach - (vb - es_) > 0 ? reach - (vb - es_) : 0);
-  // every box coordinate (offset + o[pos] + o[win]) fits comfortably in 31 bits
   for (int j = 0; j < d->in_rank; ++j) {
-    const int64_t far = d->out_size[d->pos[j]] + (d->win[j] >= 0 ? d->out_size[d->win[j]] : 0) +
-                        (d->offset[j] < 0 ? -d->offset[j] : d->offset[j]);
-    if (far > 0x3fffffffLL) return false;
+    if (ext[j] != 1) continue;
+    const int k = a.ncon++;
+    for (int f = 0; f < a.nfix; ++f)
+      if (d->pos[j] == fix_dim[f] || d->win[j] == fix_dim[f]) a.con_feed[k][f] = -1;
+    a.con_off[k] = int32_t(d->offset[j]);
+    if (checked[j]) {
+      a.con_size[k] = int32_t(d->in_size[j]);
+      a.con_bias[k] = periodic_bias(j);
+      a.con_wrap[k].init(uint32_t(d->in_size[j]));
+      a.con_chk[k] = 1;
+    }
+    a.con_stride[k] = int32_t(d->in_stride[j] * es_);  // below 2^31: reach fits in 30 bits
   }
+
+  const int nl = L.nl;
+  const int64_t* loc_ext = L.loc_ext;
+  const int64_t* loc_lds = L.loc_lds;
+  for (int k = 0; k < kTileDims; ++k) {
+    a.loc_div[k].init(uint32_t(k < nl ? loc_ext[k] : 1));
+    a.loc_lds[k] = uint32_t(k < nl ? loc_lds[k] : 0);
+  }
+  plan.nl = nl;
 
   uint64_t grid = a.blocks;
   if (grid >= 8 * kRun) grid = (grid + 8 * kRun - 1) / (8 * kRun) * (8 * kRun);
   if (grid > kU32Max) return false;
   plan.grid = uint32_t(grid);
-  plan.lds = size_t(a.box_vecs) * size_t(vb);
+  // LDS for whole groups of kUnroll * kThreads vectors
+  const uint64_t group = uint64_t(kUnroll) * kThreads;
+  plan.lds = size_t((a.box_vecs + group - 1) / group * group) * size_t(vb);
   // the output pass reads LDS below sum_k (extent_k - 1) * loc_lds[k] + vb
   uint64_t last = 0;
-  for (int k = 0; k < a.nloc; ++k) last += uint64_t(a.loc_div[k].d - 1) * a.loc_lds[k];
-  if (last + uint64_t(vb) > plan.lds) return false;
+  for (int k = 0; k < nl; ++k) last += uint64_t(loc_ext[k] - 1) * uint64_t(loc_lds[k]);
+  if (last + uint64_t(vb) > uint64_t(a.box_vecs) * uint64_t(vb)) return false;
   return true;
 }
 
@@ -783,8 +875,11 @@ bool try_window_tile(const es_gather_desc* d, const void* x, void* out, int vb, 
                      uint64_t fill, hipStream_t s, int& status) {
   TilePlan plan;
   if (!plan_window_tile(d, x, out, vb, checked, fill, plan)) return false;
-  if (plan.off32) launch_tile<int32_t>(plan.a, d->boundary, vb, plan.grid, plan.lds, s);
-  else launch_tile<int64_t>(plan.a, d->boundary, vb, plan.grid, plan.lds, s);
+  switch (d->boundary) {
+    case ES_BOUNDARY_REPLICATE: launch_tile_vb<ES_BOUNDARY_REPLICATE>(plan.a, vb, plan.nl, plan.grid, plan.lds, s); break;
+    case ES_BOUNDARY_PERIODIC: launch_tile_vb<ES_BOUNDARY_PERIODIC>(plan.a, vb, plan.nl, plan.grid, plan.lds, s); break;
+    default: launch_tile_vb<ES_BOUNDARY_CONSTANT>(plan.a, vb, plan.nl, plan.grid, plan.lds, s); break;
+  }
   set_kernel("gather_window_tile");
   status = check_launch("es_gather");
   return true;
