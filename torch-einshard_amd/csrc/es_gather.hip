@@ -415,6 +415,7 @@ constexpr int64_t kBoxBudget = 32 * 1024;  // LDS bytes per block
 constexpr int64_t kChunkMax = 64 * 1024;   // output bytes per block
 constexpr int kTileDims = 4;               // box dims of extent > 1; dims varying in a block
 constexpr uint32_t kSmallBits = 15;        // block-local indices stay below 2^15
+constexpr uint32_t kTileRun = 16;          // consecutive blocks per XCD (measured best for 3x3)
 
 // q = n / d for n < 2^kSmallBits: q = (n * m) >> s with s = kSmallBits + ceil(log2 d)
 // and m = ceil(2^s / d).  The error n (m d - 2^s) / (d 2^s) < 2^kSmallBits / 2^s <= 1/d
@@ -435,7 +436,7 @@ struct TileArgs {
   const unsigned char* x;
   unsigned char* out;
   uint64_t fill;
-  uint32_t blocks;     // real blocks (the grid is padded to whole runs of kRun per XCD)
+  uint32_t blocks;     // real blocks (the grid is padded to whole runs of kTileRun per XCD)
   uint32_t out_vecs;   // output vectors per block
   uint32_t box_vecs;   // vectors in the LDS box
   uint32_t src_limit;  // largest input byte offset a vector may start at
@@ -489,11 +490,11 @@ template <int VB, int BOUNDARY, int NL>
 __global__ __launch_bounds__(kThreads) void window_tile_kernel(const TileArgs p) {
   using V = typename Vec<VB>::type;
   extern __shared__ __align__(16) unsigned char box[];
-  // runs of kRun consecutive blocks per XCD: neighbouring tiles share input rows
+  // runs of kTileRun consecutive blocks per XCD: neighbouring tiles share input rows
   uint32_t blk = blockIdx.x;
-  if (gridDim.x % (8 * kRun) == 0) {
+  if (gridDim.x % (8 * kTileRun) == 0) {
     const uint32_t xcd = blk % 8, i = blk / 8;
-    blk = (i / kRun) * 8 * kRun + xcd * kRun + i % kRun;
+    blk = (i / kTileRun) * 8 * kTileRun + xcd * kTileRun + i % kTileRun;
   }
   if (blk >= p.blocks) return;
 
@@ -857,7 +858,7 @@ bool plan_window_tile(const es_gather_desc* d, const void* x, void* out, int vb,
   plan.nl = nl;
 
   uint64_t grid = a.blocks;
-  if (grid >= 8 * kRun) grid = (grid + 8 * kRun - 1) / (8 * kRun) * (8 * kRun);
+  if (grid >= 8 * kTileRun) grid = (grid + 8 * kTileRun - 1) / (8 * kTileRun) * (8 * kTileRun);
   if (grid > kU32Max) return false;
   plan.grid = uint32_t(grid);
   // LDS for whole groups of kUnroll * kThreads vectors
