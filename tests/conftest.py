@@ -63,8 +63,27 @@ def assert_bitexact(actual, expected):
         ev = e.contiguous().view(torch.uint8) if e.element_size() == 1 else e.contiguous().view(
             {2: torch.int16, 4: torch.int32, 8: torch.int64}[e.element_size()]
         )
-        mismatches = (av != ev).sum().item()
-        assert mismatches == 0, f"{mismatches} of {a.numel()} elements differ bitwise"
+        differ = av != ev
+        mismatches = differ.sum().item()
+        if mismatches:
+            where = differ.nonzero()[:4].tolist()
+            shown = ", ".join(
+                f"{tuple(i)}: {av[tuple(i)].item() & 0xffffffffffffffff:#x} != {ev[tuple(i)].item() & 0xffffffffffffffff:#x}"
+                for i in where
+            )
+            raise AssertionError(f"{mismatches} of {a.numel()} elements differ bitwise; first at {shown}")
+
+
+def assert_bitexact_nan(actual, expected):
+    """Bit-exact except that a NaN only has to meet a NaN: contraction outputs are one
+    rounding of the fp32 result, and torch itself rounds NaN to different bf16 bit
+    patterns (0x7FC0 in scalar code, 0xFFFF in vectorised code)."""
+    a = actual.detach().cpu()
+    e = expected.detach().cpu()
+    assert tuple(a.shape) == tuple(e.shape), (tuple(a.shape), tuple(e.shape))
+    nan_a, nan_e = a.isnan(), e.isnan()
+    assert torch.equal(nan_a, nan_e), f"NaN positions differ: {(nan_a != nan_e).sum().item()} elements"
+    assert_bitexact(a.masked_fill(nan_a, 0), e.masked_fill(nan_e, 0))
 
 
 # tolerances stated by the north star: fp32 1e-5 relative, bf16 2e-2 relative

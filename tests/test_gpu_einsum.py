@@ -13,7 +13,7 @@ from oracle.einshard_oracle import einshard_cpu
 from torch_einshard import _native
 from torch_einshard.symbolic import last_plan
 
-from conftest import TOL, assert_bitexact, assert_rel, randn
+from conftest import TOL, assert_bitexact, assert_bitexact_nan, assert_rel, gen, randn
 
 pytestmark = pytest.mark.gpu
 
@@ -325,6 +325,28 @@ def test_large_tiles_f32_m_contiguous(gpu):
     got = es.einshard("k m, n k -> m n", x.to(gpu), y.to(gpu))
     assert _native.last_kernel() == "contract_256x256"
     assert_rel(got, einshard_cpu("k m, n k -> m n", x, y), TOL[torch.float32])
+
+
+@pytest.mark.parametrize(
+    "m, n, k, kernel",
+    [(4096, 4096, 64, "contract_pipe_256x256"), (4096, 4096, 128, "contract_pipe_256x256"), (96, 80, 1, None)],
+)
+def test_output_rounding_is_bitexact(gpu, m, n, k, kernel):
+    # Only k = 0 carries values, so every output is one exact fp32 product x[m] * y[n]
+    # (a bf16 x bf16 product has at most 16 significant bits) and the result is its one
+    # rounding to bf16: nearest-even, overflow to inf, NaN stays NaN.
+    g = gen(91)
+    xv = torch.randn(m, generator=g) * 4
+    yv = torch.randn(n, generator=g) * 4
+    xv[3], xv[5], xv[11], yv[7] = float("inf"), float("nan"), 3e38, -float("inf")
+    x = torch.zeros(m, k, dtype=torch.bfloat16)
+    y = torch.zeros(n, k, dtype=torch.bfloat16)
+    x[:, 0], y[:, 0] = xv.bfloat16(), yv.bfloat16()
+    got = es.einshard("m k, n k -> m n", x.to(gpu), y.to(gpu))
+    if kernel is not None:
+        assert _native.last_kernel() == kernel
+    want = (x[:, 0].float()[:, None] * y[:, 0].float()[None, :]).bfloat16()
+    assert_bitexact_nan(got, want)
 
 
 def test_c2_pattern_repacks_one_operand(gpu):

@@ -8,6 +8,8 @@ namespace es {
 namespace contract {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -55,6 +57,12 @@ struct Traits<bf16_t> {
                                                   acc, 0, 0, 0);
   }
   static __device__ __forceinline__ S from_float(float v) { return f32_to_bf16(v); }
+  // two values rounded to nearest even and packed (v_cvt_pk_bf16_f32); a NaN stays a
+  // quiet NaN (its bit pattern is not specified: torch itself rounds NaN to 0x7FC0 in
+  // scalar code and to 0xFFFF in vectorised code)
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+  }
 };
 
 template <>
@@ -66,6 +74,9 @@ struct Traits<f16_t> {
                                                  acc, 0, 0, 0);
   }
   static __device__ __forceinline__ S from_float(float v) { return Elem<f16_t>::store(v); }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return uint32_t(from_float(a)) | (uint32_t(from_float(b)) << 16);
+  }
 };
 
 // ---- LDS tile geometry -----------------------------------------------------------
@@ -300,24 +311,43 @@ struct Loader<T, ROWS, BK, NT, kGeneric, SIDE> {
 };
 
 // ---- epilogue ------------------------------------------------------------------
-// The output group descriptors are read through a volatile pointer into the kernel
-// argument segment (the ContractArgs parameter sits at its start), so they are loaded
-// in the epilogue, where they are used, instead of being held in scalar registers
-// through the whole K loop.
+// Group descriptors read from the kernel argument segment (the ContractArgs parameter
+// sits at its start) through a constant-address-space pointer, in a loop over the
+// sub-axes that is not unrolled: the loads are uniform scalar loads issued where the
+// offsets are computed (the epilogue), and no descriptor is held in scalar registers
+// through the K loop.
+typedef const __attribute__((address_space(4))) ContractArgs* KArgs;
+typedef const __attribute__((address_space(4))) GroupArgs* KGroup;
+
+__device__ __forceinline__ KArgs kernel_args() {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
+#else
+  return nullptr;  // host pass: parsed, never executed
+#endif
+}
+
 template <int WHICH>
-__device__ __forceinline__ int64_t group_offset_v(const volatile GroupArgs& g, uint32_t i) {
+__device__ __forceinline__ int64_t group_offset_k(KGroup g, uint32_t i) {
   int64_t off = 0;
-  const int n = g.n;
+  const int n = g->n;
+#pragma nounroll
   for (int d = n - 1; d >= 0; --d) {
     FastDiv f;
-    f.d = g.div[d].d;
-    f.m = g.div[d].m;
-    f.l = g.div[d].l;
+    f.d = g->div[d].d;
+    f.m = g->div[d].m;
+    f.l = g->div[d].l;
     uint32_t r;
     i = f.divmod(i, r);
-    off += int64_t(r) * (WHICH == 0 ? g.sa[d] : (WHICH == 1 ? g.sb[d] : g.sc[d]));
+    off += int64_t(r) * (WHICH == 0 ? g->sa[d] : (WHICH == 1 ? g->sb[d] : g->sc[d]));
   }
   return off;
+}
+
+// Work-group barrier that waits for this wave's LDS operations only: global stores
+// issued before it stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // LDS bytes the epilogue needs: the staged slice plus the row / column offset tables
@@ -352,19 +382,14 @@ __device__ __forceinline__ void store_tile(const ContractArgs& p, void* lds, con
   const int wm = wave / WN;
   const int wn = wave % WN;
   S* C = static_cast<S*>(p.c);
-#if defined(__HIP_DEVICE_COMPILE__)
-  const volatile ContractArgs* kp =
-      reinterpret_cast<const volatile ContractArgs*>(__builtin_amdgcn_kernarg_segment_ptr());
-#else
-  const volatile ContractArgs* kp = &p;  // host pass: parsed, never executed
-#endif
+  const KArgs kp = kernel_args();
   for (int r = tid; r < BM; r += NT) {
     const uint32_t m = m0 + r;
-    row_off[r] = m < p.M ? boff_c + group_offset_v<2>(kp->gm, m) : -1;
+    row_off[r] = m < p.M ? boff_c + group_offset_k<2>(&kp->gm, m) : -1;
   }
   for (int c = tid; c < BN; c += NT) {
     const uint32_t n = n0 + c;
-    col_off[c] = n < p.N ? group_offset_v<2>(kp->gn, n) : -1;
+    col_off[c] = n < p.N ? group_offset_k<2>(&kp->gn, n) : -1;
   }
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
@@ -379,15 +404,13 @@ __device__ __forceinline__ void store_tile(const ContractArgs& p, void* lds, con
           *reinterpret_cast<float4*>(dst) =
               float4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
         } else {
-          const uint32_t lo = uint32_t(Traits<T>::from_float(acc[i][j][4 * g])) |
-                              (uint32_t(Traits<T>::from_float(acc[i][j][4 * g + 1])) << 16);
-          const uint32_t hi = uint32_t(Traits<T>::from_float(acc[i][j][4 * g + 2])) |
-                              (uint32_t(Traits<T>::from_float(acc[i][j][4 * g + 3])) << 16);
-          *reinterpret_cast<uint2*>(dst) = uint2{lo, hi};
+          const float v0 = acc[i][j][4 * g], v1 = acc[i][j][4 * g + 1];
+          const float v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
+          *reinterpret_cast<uint2*>(dst) = uint2{Traits<T>::pack2(v0, v1), Traits<T>::pack2(v2, v3)};
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     // staged row r is tile row (r / 32) * WTM + i * 32 + r % 32
     if (p.vstore) {
       constexpr int CV = BN / VEC;  // vectors per staged row
@@ -408,7 +431,7 @@ __device__ __forceinline__ void store_tile(const ContractArgs& p, void* lds, con
         if (ro >= 0 && co >= 0) C[ro + co] = stage[r * SLD + cn];
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
 }
 
