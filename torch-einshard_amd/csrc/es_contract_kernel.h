@@ -12,6 +12,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 // offset of linear index `i` of a group in the operand selected by WHICH
@@ -419,8 +420,10 @@ __device__ __forceinline__ void store_tile(const ContractArgs& p, void* lds, con
         const int cv = v - r * CV;
         const int64_t ro = row_off[(r / 32) * WTM + i * 32 + r % 32];
         const int64_t co = col_off[cv * VEC];
+        // nontemporal: the output is not read again by this kernel, so it is not kept in L2
         if (ro >= 0 && co >= 0)
-          *reinterpret_cast<uint4*>(C + ro + co) = *reinterpret_cast<const uint4*>(stage + r * SLD + cv * VEC);
+          __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(stage + r * SLD + cv * VEC),
+                                      reinterpret_cast<u32x4*>(C + ro + co));
       }
     } else {
       for (int v = tid; v < SROWS * BN; v += NT) {
