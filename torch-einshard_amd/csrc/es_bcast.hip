@@ -4,6 +4,11 @@
 // output dim (16-byte loads/stores when x and y are contiguous or broadcast
 // along it).  The product is formed in fp32 and rounded once, which is what
 // torch's mul does for every supported dtype, so results are bit-exact.
+//
+// The output rank is a template parameter (padded to 2, 4 or 8 with outer dims
+// of size 1), so the coordinate decomposition is straight-line code; offsets are
+// 32-bit whenever every offset fits in 31 bits.  Operands read exactly once
+// (no broadcast dim) and the output are streamed with nontemporal accesses.
 #include "es_common.h"
 
 namespace es {
@@ -22,64 +27,62 @@ struct BcastArgs {
   const void* x;
   const void* y;
   void* out;
-  uint32_t total;  // vectors
-  int32_t rank;
-  FastDiv div[kMax];  // innermost dim measured in vectors
-  int64_t sx[kMax];
+  uint32_t total;     // output vectors
+  FastDiv div[kMax];  // dims 1 .. R-1 (R-1 innermost, measured in vectors); dim 0 is not divided
+  int64_t sx[kMax];   // element strides of x per output dim
   int64_t sy[kMax];
 };
 
-template <typename T, int VEC, int XMODE, int YMODE>
 // XMODE / YMODE: 1 = contiguous along the innermost dim (vector load),
+//                3 = as 1, and every element is read exactly once (streaming load),
 //                0 = broadcast along it (one scalar, replicated),
 //                2 = strided along it (VEC scalar loads).
+// R: padded output rank, dim R-1 innermost.  OffT: int32_t when the output has
+// fewer than 2^31 vectors and every offset of x and y fits in 31 bits.
+template <typename T, int VEC, int XMODE, int YMODE, int R, typename OffT>
 __global__ __launch_bounds__(kThreads) void bcast_kernel(const BcastArgs p) {
   using S = typename Elem<T>::storage;
   const S* x = static_cast<const S*>(p.x);
   const S* y = static_cast<const S*>(p.y);
   S* out = static_cast<S*>(p.out);
+  const OffT ix = OffT(p.sx[R - 1]);
+  const OffT iy = OffT(p.sy[R - 1]);
   const uint32_t step = gridDim.x * kThreads;
   for (uint32_t v = blockIdx.x * kThreads + threadIdx.x; v < p.total; v += step) {
     uint32_t rem = v;
-    int64_t ox = 0, oy = 0;
-    uint32_t inner = 0;
+    OffT ox = 0, oy = 0;
 #pragma unroll
-    for (int d = kMax - 1; d >= 0; --d) {
-      if (d < p.rank) {
-        uint32_t r;
-        rem = p.div[d].divmod(rem, r);
-        if (d == p.rank - 1) {
-          inner = r * VEC;
-          ox += int64_t(inner) * p.sx[d];
-          oy += int64_t(inner) * p.sy[d];
-        } else {
-          ox += int64_t(r) * p.sx[d];
-          oy += int64_t(r) * p.sy[d];
-        }
-      }
+    for (int d = R - 1; d >= 1; --d) {
+      const uint32_t q = sizeof(OffT) == 4 ? p.div[d].div31(rem) : p.div[d].div(rem);
+      const OffT c = OffT(rem - q * p.div[d].d) * OffT(d == R - 1 ? VEC : 1);
+      ox += c * OffT(p.sx[d]);
+      oy += c * OffT(p.sy[d]);
+      rem = q;
     }
-    const int64_t ix = p.sx[p.rank - 1];
-    const int64_t iy = p.sy[p.rank - 1];
+    ox += OffT(rem) * OffT(p.sx[0]);  // v < total leaves the outermost coordinate
+    oy += OffT(rem) * OffT(p.sy[0]);
     S xs[VEC], ys[VEC];
     Pack<S, VEC> os;
-    if constexpr (XMODE == 1) {
-      const Pack<S, VEC> px = *reinterpret_cast<const Pack<S, VEC>*>(x + ox);
+    if constexpr (XMODE == 1 || XMODE == 3) {
+      const Pack<S, VEC>* src = reinterpret_cast<const Pack<S, VEC>*>(x + ox);
+      const Pack<S, VEC> px = XMODE == 3 ? load_nt(src) : *src;
 #pragma unroll
       for (int i = 0; i < VEC; ++i) xs[i] = px.v[i];
     } else if constexpr (XMODE == 0) {
-      S s = x[ox];
+      const S s = x[ox];
 #pragma unroll
       for (int i = 0; i < VEC; ++i) xs[i] = s;
     } else {
 #pragma unroll
       for (int i = 0; i < VEC; ++i) xs[i] = x[ox + i * ix];
     }
-    if constexpr (YMODE == 1) {
-      const Pack<S, VEC> py = *reinterpret_cast<const Pack<S, VEC>*>(y + oy);
+    if constexpr (YMODE == 1 || YMODE == 3) {
+      const Pack<S, VEC>* src = reinterpret_cast<const Pack<S, VEC>*>(y + oy);
+      const Pack<S, VEC> py = YMODE == 3 ? load_nt(src) : *src;
 #pragma unroll
       for (int i = 0; i < VEC; ++i) ys[i] = py.v[i];
     } else if constexpr (YMODE == 0) {
-      S s = y[oy];
+      const S s = y[oy];
 #pragma unroll
       for (int i = 0; i < VEC; ++i) ys[i] = s;
     } else {
@@ -88,29 +91,44 @@ __global__ __launch_bounds__(kThreads) void bcast_kernel(const BcastArgs p) {
     }
 #pragma unroll
     for (int i = 0; i < VEC; ++i) os.v[i] = Elem<T>::store(Elem<T>::load(xs[i]) * Elem<T>::load(ys[i]));
-    reinterpret_cast<Pack<S, VEC>*>(out)[v] = os;
+    store_nt(reinterpret_cast<Pack<S, VEC>*>(out) + v, os);
   }
 }
 
-template <typename T, int VEC>
-int launch_bcast(const BcastArgs& p, int xmode, int ymode, hipStream_t s, uint32_t blocks) {
-#define ES_BCAST_CASE(XM, YM)                                             \
-  if (xmode == XM && ymode == YM) {                                      \
-    bcast_kernel<T, VEC, XM, YM><<<blocks, kThreads, 0, s>>>(p);         \
-    set_kernel("bcast_" #XM #YM);                                        \
-    return check_launch("es_bcast");                                     \
+// 16-byte vectors, rank 2 or 4, 32-bit offsets: every mode pair
+template <typename T, int R>
+int launch_fast(const BcastArgs& p, int xmode, int ymode, hipStream_t s, uint32_t blocks) {
+  constexpr int VEC = 16 / int(sizeof(typename Elem<T>::storage));
+#define ES_BCAST_CASE(XM, YM)                                                    \
+  if (xmode == XM && ymode == YM) {                                             \
+    bcast_kernel<T, VEC, XM, YM, R, int32_t><<<blocks, kThreads, 0, s>>>(p);    \
+    set_kernel("bcast_" #XM #YM);                                               \
+    return check_launch("es_bcast");                                            \
   }
-  ES_BCAST_CASE(1, 1)
-  ES_BCAST_CASE(1, 0)
-  ES_BCAST_CASE(0, 1)
-  ES_BCAST_CASE(0, 0)
-  ES_BCAST_CASE(2, 2)
-  ES_BCAST_CASE(1, 2)
-  ES_BCAST_CASE(2, 1)
-  ES_BCAST_CASE(2, 0)
-  ES_BCAST_CASE(0, 2)
+  ES_BCAST_CASE(0, 0) ES_BCAST_CASE(0, 1) ES_BCAST_CASE(0, 2) ES_BCAST_CASE(0, 3)
+  ES_BCAST_CASE(1, 0) ES_BCAST_CASE(1, 1) ES_BCAST_CASE(1, 2) ES_BCAST_CASE(1, 3)
+  ES_BCAST_CASE(2, 0) ES_BCAST_CASE(2, 1) ES_BCAST_CASE(2, 2) ES_BCAST_CASE(2, 3)
+  ES_BCAST_CASE(3, 0) ES_BCAST_CASE(3, 1) ES_BCAST_CASE(3, 2) ES_BCAST_CASE(3, 3)
 #undef ES_BCAST_CASE
   return fail(ES_ERR_INVALID, "es_bcast: bad stride mode");
+}
+
+// everything else: one element per thread, rank 8, 64-bit offsets
+template <typename T>
+int launch_general(const BcastArgs& p, int xmode, int ymode, hipStream_t s, uint32_t blocks) {
+  set_kernel("bcast_scalar");
+  if (xmode == 0 && ymode == 0) bcast_kernel<T, 1, 0, 0, kMax, int64_t><<<blocks, kThreads, 0, s>>>(p);
+  else if (xmode == 0) bcast_kernel<T, 1, 0, 2, kMax, int64_t><<<blocks, kThreads, 0, s>>>(p);
+  else if (ymode == 0) bcast_kernel<T, 1, 2, 0, kMax, int64_t><<<blocks, kThreads, 0, s>>>(p);
+  else bcast_kernel<T, 1, 2, 2, kMax, int64_t><<<blocks, kThreads, 0, s>>>(p);
+  return check_launch("es_bcast");
+}
+
+template <typename T>
+int launch_typed(const BcastArgs& p, bool fast, int r, int xmode, int ymode, hipStream_t s, uint32_t blocks) {
+  if (!fast) return launch_general<T>(p, xmode, ymode, s, blocks);
+  if (r == 2) return launch_fast<T, 2>(p, xmode, ymode, s, blocks);
+  return launch_fast<T, 4>(p, xmode, ymode, s, blocks);
 }
 
 }  // namespace
@@ -130,10 +148,6 @@ extern "C" int es_bcast(const es_bcast_desc* d, const void* x, const void* y, vo
   if (total == 0) return ES_OK;
   if (x == nullptr || y == nullptr || out == nullptr) return fail(ES_ERR_INVALID, "es_bcast: null pointer");
 
-  BcastArgs p;
-  p.x = x;
-  p.y = y;
-  p.out = out;
   // a rank-0 descriptor is a single element: run it as one dim of size 1
   es_axis axes[kMax];
   int rank = d->rank;
@@ -142,67 +156,67 @@ extern "C" int es_bcast(const es_bcast_desc* d, const void* x, const void* y, vo
     axes[0] = es_axis{1, 0, 0, 0};
     rank = 1;
   }
-  p.rank = rank;
   const es_axis& in = axes[rank - 1];
 
-  // vector width along the innermost dim
+  // 16-byte vectors along the innermost dim, when sizes, strides and pointers allow
   const int max_vec = 16 / esz;
-  int vec = 1;
-  for (int cand = max_vec; cand > 1; cand /= 2) {
-    if (in.size % cand != 0) continue;
-    if (!aligned(out, cand * esz)) continue;
-    bool ok = true;
-    for (int i = 0; i < rank - 1 && ok; ++i)
-      if (axes[i].a % cand != 0 || axes[i].b % cand != 0) ok = false;
-    if (in.a == 1 && !aligned(x, cand * esz)) ok = false;
-    if (in.b == 1 && !aligned(y, cand * esz)) ok = false;
-    if (ok) {
-      vec = cand;
-      break;
-    }
+  bool wide = in.size % max_vec == 0 && aligned(out, 16);
+  for (int i = 0; i < rank - 1 && wide; ++i)
+    if (axes[i].a % max_vec != 0 || axes[i].b % max_vec != 0) wide = false;
+  if (in.a == 1 && !aligned(x, 16)) wide = false;
+  if (in.b == 1 && !aligned(y, 16)) wide = false;
+
+  // an operand with no broadcast (zero-stride) dim is read exactly once: stream it
+  bool x_once = true, y_once = true;
+  uint64_t reach_x = 0, reach_y = 0;  // largest |offset| in elements
+  for (int i = 0; i < rank; ++i) {
+    if (axes[i].size > 1 && axes[i].a == 0) x_once = false;
+    if (axes[i].size > 1 && axes[i].b == 0) y_once = false;
+    reach_x += uint64_t(axes[i].size - 1) * uint64_t(axes[i].a < 0 ? -axes[i].a : axes[i].a);
+    reach_y += uint64_t(axes[i].size - 1) * uint64_t(axes[i].b < 0 ? -axes[i].b : axes[i].b);
   }
-  const int xmode = in.a == 1 ? 1 : (in.a == 0 ? 0 : 2);
-  const int ymode = in.b == 1 ? 1 : (in.b == 0 ? 0 : 2);
-  int xm = xmode, ym = ymode;
-  if (vec == 1) {  // scalar path: a strided load covers every case
-    xm = xmode == 0 ? 0 : 2;
-    ym = ymode == 0 ? 0 : 2;
-  }
+  const int xmode = in.a == 1 ? (x_once ? 3 : 1) : (in.a == 0 ? 0 : 2);
+  const int ymode = in.b == 1 ? (y_once ? 3 : 1) : (in.b == 0 ? 0 : 2);
+  // fast path: 16-byte vectors, rank <= 4, 32-bit offsets; otherwise one element per
+  // thread with 64-bit offsets
+  const uint64_t lim31 = uint64_t(1) << 31;
+  const bool fast = wide && rank <= 4 && total / uint64_t(max_vec) < lim31 && reach_x + max_vec < lim31 &&
+                    reach_y + max_vec < lim31;
+  const int vec = fast ? max_vec : 1;
+  const int r = fast ? (rank <= 2 ? 2 : 4) : kMax;
   const uint64_t total_vec = total / uint64_t(vec);
   if (total_vec > kU32Max) return fail(ES_ERR_UNSUPPORTED, "es_bcast: output too large");
+
+  BcastArgs p;
+  p.x = x;
+  p.y = y;
+  p.out = out;
   p.total = uint32_t(total_vec);
-  for (int i = 0; i < kMax; ++i) {
-    if (i < rank) {
+  // descriptor dim i lands at padded dim i + (r - rank); the padding dims have size 1
+  for (int j = 0; j < kMax; ++j) {
+    const int i = j - (r - rank);
+    if (j < r && i >= 0) {
       int64_t s = axes[i].size;
       if (i == rank - 1) s /= vec;
       if (uint64_t(s) > kU32Max) return fail(ES_ERR_UNSUPPORTED, "es_bcast: dim too large");
-      p.div[i].init(uint32_t(s));
-      p.sx[i] = axes[i].a;
-      p.sy[i] = axes[i].b;
+      p.div[j].init(uint32_t(s));
+      p.sx[j] = axes[i].a;
+      p.sy[j] = axes[i].b;
     } else {
-      p.div[i].init(1);
-      p.sx[i] = 0;
-      p.sy[i] = 0;
+      p.div[j].init(1);
+      p.sx[j] = 0;
+      p.sy[j] = 0;
     }
   }
   const uint64_t blocks64 = (total_vec + kThreads - 1) / kThreads;
   const uint32_t blocks = uint32_t(blocks64 > 1048576 ? 1048576 : blocks64);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int xm = fast ? xmode : (xmode == 0 ? 0 : 2);
+  const int ym = fast ? ymode : (ymode == 0 ? 0 : 2);
   switch (d->dtype) {
-    case ES_F32:
-      if (vec == 4) return launch_bcast<float, 4>(p, xm, ym, s, blocks);
-      if (vec == 2) return launch_bcast<float, 2>(p, xm, ym, s, blocks);
-      return launch_bcast<float, 1>(p, xm, ym, s, blocks);
-    case ES_BF16:
-      if (vec == 8) return launch_bcast<bf16_t, 8>(p, xm, ym, s, blocks);
-      if (vec == 4) return launch_bcast<bf16_t, 4>(p, xm, ym, s, blocks);
-      if (vec == 2) return launch_bcast<bf16_t, 2>(p, xm, ym, s, blocks);
-      return launch_bcast<bf16_t, 1>(p, xm, ym, s, blocks);
-    case ES_F16:
-      if (vec == 8) return launch_bcast<f16_t, 8>(p, xm, ym, s, blocks);
-      if (vec == 4) return launch_bcast<f16_t, 4>(p, xm, ym, s, blocks);
-      if (vec == 2) return launch_bcast<f16_t, 2>(p, xm, ym, s, blocks);
-      return launch_bcast<f16_t, 1>(p, xm, ym, s, blocks);
+    case ES_F32: return launch_typed<float>(p, fast, r, xm, ym, s, blocks);
+    case ES_BF16: return launch_typed<bf16_t>(p, fast, r, xm, ym, s, blocks);
+    case ES_F16: return launch_typed<f16_t>(p, fast, r, xm, ym, s, blocks);
   }
   return fail(ES_ERR_UNSUPPORTED, "es_bcast: unsupported dtype");
 }

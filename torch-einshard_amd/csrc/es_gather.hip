@@ -188,7 +188,7 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(const GatherArgs p) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint32_t v = base + u * kThreads + threadIdx.x;
-      if (v < p.total) reinterpret_cast<V*>(p.out)[v] = select_vec(keep[u], value[u], fillv);
+      if (v < p.total) store_nt(reinterpret_cast<V*>(p.out) + v, select_vec(keep[u], value[u], fillv));
     }
   }
 }
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(const TransposeArgs a) {
     for (int v = threadIdx.x; v < kTileQ * RV; v += 256) {
       const int q = v / RV, pv = (v - q * RV) * VEC;
       if (p0 + pv < a.size_p && q0 + q < a.size_q) {
-        const V val = *reinterpret_cast<const V*>(x + in_base + int64_t(q0 + q) * a.q_in_stride + p0 + pv);
+        const V val = load_nt(reinterpret_cast<const V*>(x + in_base + int64_t(q0 + q) * a.q_in_stride + p0 + pv));
 #pragma unroll
         for (int e = 0; e < VEC; ++e) tile[q][pv + e] = val.v[e];
       }
@@ -292,7 +292,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(const TransposeArgs a) {
         V val;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) val.v[e] = tile[qv + e][p];
-        *reinterpret_cast<V*>(out + out_base + int64_t(p0 + p) * a.p_out_stride + q0 + qv) = val;
+        store_nt(reinterpret_cast<V*>(out + out_base + int64_t(p0 + p) * a.p_out_stride + q0 + qv), val);
       }
     }
     __syncthreads();
@@ -596,10 +596,10 @@ __global__ __launch_bounds__(kThreads) void window_tile_kernel(const TileArgs p)
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) value[u] = *reinterpret_cast<const V*>(box + off[u]);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) out[first + u * kThreads + threadIdx.x] = value[u];
+    for (int u = 0; u < kUnroll; ++u) store_nt(out + first + u * kThreads + threadIdx.x, value[u]);
   }
   for (uint32_t i = first + threadIdx.x; i < p.out_vecs; i += kThreads)
-    out[i] = *reinterpret_cast<const V*>(box + lds_of(i));
+    store_nt(out + i, *reinterpret_cast<const V*>(box + lds_of(i)));
 }
 
 template <int VB, int BOUNDARY>

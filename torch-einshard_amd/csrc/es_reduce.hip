@@ -14,7 +14,9 @@
 //    outputs are split over work-groups the same way.
 //
 // The summation order is a fixed function of the descriptor (deterministic);
-// each thread adds its terms in increasing reduced-index order.
+// each thread adds its terms in increasing reduced-index order.  x is read with
+// streaming (nontemporal) loads and the result written with streaming stores:
+// each element of x is read exactly once.
 #include "es_common.h"
 
 namespace es {
@@ -104,12 +106,12 @@ __global__ __launch_bounds__(kThreads) void reduce_cols(const ReduceArgs p, cons
     offsets(r, p.n_redax, p.red_div, p.red_sx, p.red_sy, rx, ry, 1);
     const int64_t bx = kx + rx;
     if constexpr (XMODE == 1) {
-      const Pack<S, VEC> v = *reinterpret_cast<const Pack<S, VEC>*>(x + bx);
+      const Pack<S, VEC> v = load_nt(reinterpret_cast<const Pack<S, VEC>*>(x + bx));
 #pragma unroll
       for (int i = 0; i < VEC; ++i) xv[i] = Elem<T>::load(v.v[i]);
     } else {
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) xv[i] = Elem<T>::load(x[bx + i * ix]);
+      for (int i = 0; i < VEC; ++i) xv[i] = Elem<T>::load(load_nt(x + bx + i * ix));
     }
     if constexpr (HAS_Y) {
       const int64_t by = ky + ry;
@@ -170,7 +172,7 @@ __global__ __launch_bounds__(kThreads) void reduce_cols(const ReduceArgs p, cons
     Pack<S, VEC> o;
 #pragma unroll
     for (int i = 0; i < VEC; ++i) o.v[i] = Elem<T>::store(acc[i]);
-    reinterpret_cast<Pack<S, VEC>*>(p.out)[vcol] = o;
+    store_nt(reinterpret_cast<Pack<S, VEC>*>(p.out) + vcol, o);
   }
 }
 
@@ -197,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void reduce_rows(const ReduceArgs p) {
   auto load = [&](uint32_t r, Pack<S, VEC>& xv, float (&yv)[VEC]) {
     int64_t rx, ry;
     offsets(r, p.n_redax, p.red_div, p.red_sx, p.red_sy, rx, ry, VEC);
-    xv = *reinterpret_cast<const Pack<S, VEC>*>(x + kx + rx);
+    xv = load_nt(reinterpret_cast<const Pack<S, VEC>*>(x + kx + rx));
     if constexpr (HAS_Y) {
       if constexpr (YMODE == 1) {
         const Pack<S, VEC> v = *reinterpret_cast<const Pack<S, VEC>*>(y + ky + ry);
