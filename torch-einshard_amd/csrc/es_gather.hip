@@ -16,6 +16,7 @@
 // Elements move as raw bits, so the copy is bit-exact for any element type.
 // The kernel is HBM-bound: each output byte is written once; a 3x3 window
 // re-reads each input element 9 times, from L2.
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -415,7 +416,7 @@ constexpr int64_t kBoxBudget = 32 * 1024;  // LDS bytes per block
 constexpr int64_t kChunkMax = 64 * 1024;   // output bytes per block
 constexpr int kTileDims = 4;               // box dims of extent > 1; dims varying in a block
 constexpr uint32_t kSmallBits = 15;        // block-local indices stay below 2^15
-constexpr uint32_t kTileRun = 16;          // consecutive blocks per XCD (measured best for 3x3)
+constexpr uint32_t kTileRunMax = 1u << 30;  // consecutive blocks per XCD (whole bands measured best)
 
 // q = n / d for n < 2^kSmallBits: q = (n * m) >> s with s = kSmallBits + ceil(log2 d)
 // and m = ceil(2^s / d).  The error n (m d - 2^s) / (d 2^s) < 2^kSmallBits / 2^s <= 1/d
@@ -436,7 +437,8 @@ struct TileArgs {
   const unsigned char* x;
   unsigned char* out;
   uint64_t fill;
-  uint32_t blocks;     // real blocks (the grid is padded to whole runs of kTileRun per XCD)
+  uint32_t blocks;     // real blocks (the grid is padded to whole runs per XCD)
+  uint32_t run;        // consecutive blocks per XCD; 0: hardware order
   uint32_t out_vecs;   // output vectors per block
   uint32_t box_vecs;   // vectors in the LDS box
   uint32_t src_limit;  // largest input byte offset a vector may start at
@@ -490,11 +492,11 @@ template <int VB, int BOUNDARY, int NL>
 __global__ __launch_bounds__(kThreads) void window_tile_kernel(const TileArgs p) {
   using V = typename Vec<VB>::type;
   extern __shared__ __align__(16) unsigned char box[];
-  // runs of kTileRun consecutive blocks per XCD: neighbouring tiles share input rows
+  // runs of p.run consecutive blocks per XCD: neighbouring tiles share input rows
   uint32_t blk = blockIdx.x;
-  if (gridDim.x % (8 * kTileRun) == 0) {
+  if (p.run > 0) {
     const uint32_t xcd = blk % 8, i = blk / 8;
-    blk = (i / kTileRun) * 8 * kTileRun + xcd * kTileRun + i % kTileRun;
+    blk = (i / p.run) * 8 * p.run + xcd * p.run + i % p.run;
   }
   if (blk >= p.blocks) return;
 
@@ -858,7 +860,12 @@ bool plan_window_tile(const es_gather_desc* d, const void* x, void* out, int vb,
   plan.nl = nl;
 
   uint64_t grid = a.blocks;
-  if (grid >= 8 * kTileRun) grid = (grid + 8 * kTileRun - 1) / (8 * kTileRun) * (8 * kTileRun);
+  a.run = 0;
+  if (grid >= 8) {
+    const uint64_t run = std::min<uint64_t>((grid + 7) / 8, kTileRunMax);
+    a.run = uint32_t(run);
+    grid = (grid + 8 * run - 1) / (8 * run) * (8 * run);
+  }
   if (grid > kU32Max) return false;
   plan.grid = uint32_t(grid);
   // LDS for whole groups of kUnroll * kThreads vectors
