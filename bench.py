@@ -16,8 +16,8 @@ kernel's average duration (roofline.achieved) comes from HIP events recorded on
 the stream the kernel runs on (torch's current stream, which the library
 launches on) around K more launches queued behind a bounded spin kernel, so
 they run back to back without host gaps.  For HBM-bound workloads K more
-launches follow, each after a 512 MiB fill that evicts the 256 MB Infinity
-Cache (fill not timed): roofline.kernel_ms_cold.
+launches follow, each after a 512 MiB read that evicts the 256 MB Infinity
+Cache (not timed): roofline.kernel_ms_cold.
 
 roofline.achieved uses algorithmic work only: 2*M*N*K flops for contractions,
 unique input bytes + output bytes for the copy / reduce / broadcast kernels.
@@ -255,12 +255,13 @@ def measure_gpu(es, wl, dev, steps, warmup):
     cold_ms = None
     if wl["bound"] == "hbm":
         # the same launches with the 256 MB Infinity Cache flushed before each
-        # one (a 512 MiB fill, not timed): shows whether back-to-back steps were
-        # served from cache
-        flush = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev)
+        # one (a 512 MiB read, not timed; a read leaves no dirty lines behind to
+        # be written back during the timed launch): shows whether back-to-back
+        # steps were served from cache
+        flush = torch.ones(512 * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
         events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
         for s, e in events:
-            flush.fill_(1)
+            flush.sum()
             s.record(stream)
             out = run(xs)
             e.record(stream)

@@ -156,7 +156,9 @@ __device__ __forceinline__ OffT source_of(const GatherArgs& p, uint32_t v, bool&
 constexpr int kUnroll = 4;
 constexpr uint32_t kRun = 64;  // consecutive work-groups per XCD
 
-template <int VB, int R, typename OffT, int BOUNDARY, bool M24>
+// NT: every input element is read at most once (no window, no broadcast, constant
+// boundary), so the input is read with streaming loads.
+template <int VB, int R, typename OffT, int BOUNDARY, bool M24, bool NT>
 __global__ __launch_bounds__(kThreads) void gather_kernel(const GatherArgs p) {
   using V = typename Vec<VB>::type;
   const uint32_t chunk = kUnroll * kThreads;
@@ -185,7 +187,10 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(const GatherArgs p) {
     }
     V value[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) value[u] = *reinterpret_cast<const V*>(p.x + src[u]);
+    for (int u = 0; u < kUnroll; ++u) {
+      const V* a = reinterpret_cast<const V*>(p.x + src[u]);
+      value[u] = NT ? load_nt(a) : *a;
+    }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint32_t v = base + u * kThreads + threadIdx.x;
@@ -197,13 +202,22 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(const GatherArgs p) {
 // index arithmetic of a launch: 64-bit offsets, 32-bit, or 32-bit with 24-bit multiplies
 enum class Index { k64, k32, k24 };
 
-template <int VB, typename OffT, int BOUNDARY, bool M24>
+template <int VB, typename OffT, int BOUNDARY, bool M24, bool NT = false>
 void launch_rank(const GatherArgs& p, uint32_t blocks, hipStream_t s) {
   switch (p.out_rank) {
-    case 2: gather_kernel<VB, 2, OffT, BOUNDARY, M24><<<blocks, kThreads, 0, s>>>(p); break;
-    case 4: gather_kernel<VB, 4, OffT, BOUNDARY, M24><<<blocks, kThreads, 0, s>>>(p); break;
-    case 6: gather_kernel<VB, 6, OffT, BOUNDARY, M24><<<blocks, kThreads, 0, s>>>(p); break;
-    default: gather_kernel<VB, 8, OffT, BOUNDARY, M24><<<blocks, kThreads, 0, s>>>(p); break;
+    case 2: gather_kernel<VB, 2, OffT, BOUNDARY, M24, NT><<<blocks, kThreads, 0, s>>>(p); break;
+    case 4: gather_kernel<VB, 4, OffT, BOUNDARY, M24, NT><<<blocks, kThreads, 0, s>>>(p); break;
+    case 6: gather_kernel<VB, 6, OffT, BOUNDARY, M24, NT><<<blocks, kThreads, 0, s>>>(p); break;
+    default: gather_kernel<VB, 8, OffT, BOUNDARY, M24, NT><<<blocks, kThreads, 0, s>>>(p); break;
+  }
+}
+
+// 16-byte vectors whose input elements are each read at most once: streaming loads
+void launch_stream16(const GatherArgs& p, Index index, uint32_t blocks, hipStream_t s) {
+  switch (index) {
+    case Index::k64: launch_rank<16, int64_t, ES_BOUNDARY_CONSTANT, false, true>(p, blocks, s); break;
+    case Index::k32: launch_rank<16, int32_t, ES_BOUNDARY_CONSTANT, false, true>(p, blocks, s); break;
+    default: launch_rank<16, int32_t, ES_BOUNDARY_CONSTANT, true, true>(p, blocks, s); break;
   }
 }
 
@@ -1084,8 +1098,21 @@ extern "C" int es_gather(const es_gather_desc* d, const void* x, void* out, void
                                            {"gather_v16_o64", "gather_v16", "gather_v16_m24"}};
   int vb_log = 0;
   while ((1 << vb_log) < vb) ++vb_log;
+  // every input element read at most once: a constant boundary, no window, and each
+  // output dim feeding exactly one input dim (a permutation, possibly padded)
+  bool once = d->boundary == ES_BOUNDARY_CONSTANT;
+  for (int o = 0; o < d->out_rank && once; ++o) {
+    int feeds = 0;
+    for (int j = 0; j < d->in_rank; ++j) feeds += (d->pos[j] == o) + (d->win[j] == o);
+    if (feeds != 1) once = false;
+  }
+  for (int j = 0; j < d->in_rank && once; ++j)
+    if (d->win[j] >= 0) once = false;
   switch (vb) {
-    case 16: launch_vb<16>(p, index, d->boundary, blocks, s); break;
+    case 16:
+      if (once) launch_stream16(p, index, blocks, s);
+      else launch_vb<16>(p, index, d->boundary, blocks, s);
+      break;
     case 8: launch_vb<8>(p, index, d->boundary, blocks, s); break;
     case 4: launch_vb<4>(p, index, d->boundary, blocks, s); break;
     case 2: launch_vb<2>(p, index, d->boundary, blocks, s); break;
