@@ -204,5 +204,8 @@ constexpr uint64_t kU32Max = 0xffffffffull;
 // busy with several resident groups; fixed so that sizing decisions are a
 // pure function of the descriptor.
 constexpr int kTargetGroups = 256 * 8;
+// Compute units of an MI355X: tile-count decisions assume them, so they too are a
+// pure function of the descriptor.
+constexpr int kCUs = 256;
 
 }  // namespace es

@@ -27,6 +27,9 @@
 //     4 waves of 128 x 128, two LDS stages filled by global_load_lds_dwordx4
 //     copies issued a full K tile ahead, an explicit MFMA / LDS-read / copy
 //     interleave (see es_contract_kernel.h);
+//   * contract_pipe16 (the same operands, 256 x 224 tiles): the pipeline on
+//     v_mfma_f32_16x16x32 with waves of 128 x 112, chosen when an N extent cuts into
+//     fewer rounds of one tile per CU than with 256-wide tiles (N = 1792);
 //   * contract_kernel (every other case): WM x WN waves over a BM x BN tile,
 //     double-buffered LDS with one barrier per K tile.  Its loaders:
 //       - K-contiguous: direct global -> LDS copies;
@@ -58,6 +61,7 @@ struct ContractArgs {
   uint32_t tiles_m, tiles_n;
   uint32_t group_n;      // N-tiles per tile group (divides tiles_n; see tile_of)
   uint32_t total_tiles;
+  uint32_t pipe_bn;      // 224: the 256 x 224 tiles of contract_pipe16; 0 otherwise
   int32_t vstore;        // 16-byte vector stores along n
   int32_t off32;         // every byte offset into A and B fits in 32 bits
   uint32_t k_inner;      // extent of the innermost K sub-axis (fast paths: a multiple of BK)

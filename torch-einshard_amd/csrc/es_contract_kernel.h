@@ -4,6 +4,8 @@
 
 #include "es_contract.h"
 
+#include <type_traits>
+
 namespace es {
 namespace contract {
 
@@ -12,6 +14,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -842,6 +845,267 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   store_tile<T, BM, BN, WM, WN>(p, lds0, acc, m0, n0, boff_c);
 }
 
+// ---- 16x16x32 pipelined kernel: 256 x BN tiles, BN = 256 or 224 ---------------------
+// The pipeline of contract_pipe on v_mfma_f32_16x16x32_{bf16,f16}: four waves (2 x 2)
+// each own 128 x BN/2 as 8 x BN/32 blocks of 16 x 16, and a 64-deep K tile is two
+// substeps of 32.  Blocks of 16 allow BN = 224 (waves of 128 x 112): an N extent of
+// 7 x 256 = 1792 (one tensor-parallel rank's share of a 14336-wide weight) then cuts
+// into 8 tiles instead of 7, and 16384 x 1792 into 512 tiles, two whole rounds of one
+// tile per CU, where 256 x 256 tiles leave a quarter of the CUs idle in the second.
+// Lane l of a fragment read holds k = 8 * (l / 16) .. +7 of row l % 16 (one 16-byte LDS
+// read); the first MFMA operand is the N-side fragment, so the accumulator holds C^T and
+// lane l ends with 4 consecutive n (4 * (l / 16) + 0..3) of m = l % 16.
+// MFMAs of contract_pipe16 as inline assembly with the accumulator tied to the result
+// ("+a": read and written in place, in AGPRs).  The builtin is selected in a form
+// whose result need not share the accumulator's registers, and with 56 accumulators
+// per wave the register allocator then rotated them through the AGPRs with a copy per
+// accumulator per K tile (measured 40 % slower).  The compiler cannot see hazards across
+// inline assembly, so the kernel avoids them by construction: nothing but these MFMAs
+// writes the accumulators (the first MFMA of a tile takes the constant 0 as its
+// accumulator, mma_first), the fragment operands come straight from LDS reads, and
+// pipe16_drain separates the last MFMA from the first VALU read of a result.
+template <typename T>
+struct Mma16;
+
+template <>
+struct Mma16<bf16_t> {
+  static __device__ __forceinline__ void mma(f32x4& acc, const uint4& nfrag, const uint4& mfrag) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                 : "+a"(acc)
+                 : "v"(__builtin_bit_cast(u32x4, nfrag)), "v"(__builtin_bit_cast(u32x4, mfrag)));
+  }
+  static __device__ __forceinline__ void mma_first(f32x4& acc, const uint4& nfrag, const uint4& mfrag) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0"
+                 : "=a"(acc)
+                 : "v"(__builtin_bit_cast(u32x4, nfrag)), "v"(__builtin_bit_cast(u32x4, mfrag)));
+  }
+};
+
+template <>
+struct Mma16<f16_t> {
+  static __device__ __forceinline__ void mma(f32x4& acc, const uint4& nfrag, const uint4& mfrag) {
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"
+                 : "+a"(acc)
+                 : "v"(__builtin_bit_cast(u32x4, nfrag)), "v"(__builtin_bit_cast(u32x4, mfrag)));
+  }
+  static __device__ __forceinline__ void mma_first(f32x4& acc, const uint4& nfrag, const uint4& mfrag) {
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0"
+                 : "=a"(acc)
+                 : "v"(__builtin_bit_cast(u32x4, nfrag)), "v"(__builtin_bit_cast(u32x4, mfrag)));
+  }
+};
+
+// After the last MFMA of a tile: 32 wait states (more than any 16x16x32 result needs
+// before a VALU read), then every accumulator passes through an empty statement that
+// follows them, so no read of a result can be scheduled before the wait.
+template <int FM, int FN>
+__device__ __forceinline__ void pipe16_drain(f32x4 (&acc)[FM][FN]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) asm volatile("" : "+a"(acc[i][j]));
+}
+
+// Epilogue of contract_pipe16: eight passes of 32 tile rows.  Pass q stages rows
+// wm * 128 + 32 * (q % 4) + 0..31 (wm = q / 4), written by the two waves of wave row wm
+// as [row][n] in `lds`, then the whole work-group writes them out (16-byte streaming
+// stores along n when n is the output's contiguous axis, element stores otherwise).
+// The caller has drained every copy into LDS and synchronised the work-group.
+template <typename T, int BN, int FM, int FN>
+__device__ __forceinline__ void store_tile16(const ContractArgs& p, void* lds, const f32x4 (&acc)[FM][FN], uint32_t m0,
+                                             uint32_t n0, int64_t boff_c) {
+  using S = typename Traits<T>::S;
+  constexpr int BM = 256, WTM = 128, WTN = BN / 2, VEC = 8, NT = 256;
+  constexpr int SROWS = 32;
+  constexpr int SLD = BN + VEC;  // staging row pitch (elements)
+  S* stage = static_cast<S*>(lds);
+  int64_t* row_off = reinterpret_cast<int64_t*>(static_cast<char*>(lds) + SROWS * SLD * int(sizeof(S)));
+  int64_t* col_off = row_off + BM;
+  const int tid = threadIdx.x;
+  const int lane = tid % 64;
+  const int wave = tid / 64;
+  const int wm = wave / 2;
+  const int wn = wave % 2;
+  S* C = static_cast<S*>(p.c);
+  const KArgs kp = kernel_args();
+  for (int r = tid; r < BM; r += NT) {
+    const uint32_t m = m0 + r;
+    row_off[r] = m < p.M ? boff_c + group_offset_k<2>(&kp->gm, m) : -1;
+  }
+  for (int c = tid; c < BN; c += NT) {
+    const uint32_t n = n0 + c;
+    col_off[c] = n < p.N ? group_offset_k<2>(&kp->gn, n) : -1;
+  }
+#pragma unroll
+  for (int q = 0; q < 2 * FM / 2; ++q) {
+    const int pw = q / (FM / 2);
+    const int i0 = 2 * (q % (FM / 2));
+    if (wm == pw) {
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const f32x4& a = acc[i0 + ii][j];
+          *reinterpret_cast<uint2*>(stage + (ii * 16 + lane % 16) * SLD + wn * WTN + j * 16 + 4 * (lane / 16)) =
+              uint2{Traits<T>::pack2(a[0], a[1]), Traits<T>::pack2(a[2], a[3])};
+        }
+    }
+    lds_barrier();
+    const int row0 = pw * WTM + i0 * 16;  // tile row of staged row 0
+    if (p.vstore) {
+      constexpr int CV = BN / VEC;  // vectors per staged row
+      for (int v = tid; v < SROWS * CV; v += NT) {
+        const int r = v / CV;
+        const int cv = v - r * CV;
+        const int64_t ro = row_off[row0 + r];
+        const int64_t co = col_off[cv * VEC];
+        // nontemporal: the output is not read again by this kernel, so it is not kept in L2
+        if (ro >= 0 && co >= 0)
+          __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(stage + r * SLD + cv * VEC),
+                                      reinterpret_cast<u32x4*>(C + ro + co));
+      }
+    } else {
+      for (int v = tid; v < SROWS * BN; v += NT) {
+        const int r = v / BN;
+        const int cn = v - r * BN;
+        const int64_t ro = row_off[row0 + r];
+        const int64_t co = col_off[cn];
+        if (ro >= 0 && co >= 0) C[ro + co] = stage[r * SLD + cn];
+      }
+    }
+    lds_barrier();
+  }
+}
+
+template <typename T, int BN>
+__global__ __launch_bounds__(256, 1) void contract_pipe16(const ContractArgs p) {
+  using S = typename Traits<T>::S;
+  constexpr int BM = 256, WM = 2, WN = 2;
+  constexpr int VEC = 8;
+  constexpr int BK = kRowBytes / int(sizeof(S));  // 64
+  constexpr int NS = BK / 32;                      // substeps of 32 k
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int MMAS = FM * FN;  // per substep
+  using CopyA = PipeCopies<S, BM, WM * WN, 0>;
+  using CopyB = PipeCopies<S, BN, WM * WN, 1>;
+  constexpr int NCOPY = CopyA::NI + CopyB::NI;  // copies per wave per K tile
+  static_assert(sizeof(S) == 2 && NS == 2, "16-bit element types, two substeps per K tile");
+  static_assert(WTN % 16 == 0 && FM % 2 == 0, "tile shape");
+  static_assert(NCOPY <= MMAS && FM + FN <= MMAS, "last substep interleave");
+  static_assert(32 * (BN + VEC) * int(sizeof(S)) + (BM + BN) * 8 <= int(sizeof(S)) * STAGE, "epilogue fits a stage");
+
+  __shared__ __attribute__((aligned(1024))) S lds0[STAGE];
+  __shared__ __attribute__((aligned(1024))) S lds1[STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % 64;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+
+  uint32_t bidx, tm, tn;
+  tile_of(p, blockIdx.x, bidx, tm, tn);
+  const uint32_t m0 = tm * BM;
+  const uint32_t n0 = tn * BN;
+  const int64_t boff_a = group_offset<0>(p.gb, bidx);
+  const int64_t boff_b = group_offset<1>(p.gb, bidx);
+  const int64_t boff_c = group_offset<2>(p.gb, bidx);
+
+  CopyA ca;
+  CopyB cb;
+  ca.init(p, wave, lane, m0, boff_a);
+  cb.init(p, wave, lane, n0, boff_b);
+
+  f32x4 acc[FM][FN];  // first written by mma_first
+
+  // fragment rows of this lane are lane % 16 plus multiples of 16: one swizzle key
+  const int lrow = lane % 16;
+  int kofs[NS];
+#pragma unroll
+  for (int ks = 0; ks < NS; ++ks) kofs[ks] = lrow * BK + swz(lrow, ks * 4 + lane / 16) * VEC;
+  const int abase = wm * WTM * BK;
+  const int bbase = BM * BK + wn * WTN * BK;
+
+  uint4 af[2][FM], bf[2][FN];
+  auto frags = [&](const S* stage, int buf, int ks) {
+    const S* a = stage + abase + kofs[ks];
+    const S* b = stage + bbase + kofs[ks];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const uint4*>(a + i * 16 * BK);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[buf][j] = *reinterpret_cast<const uint4*>(b + j * 16 * BK);
+  };
+
+  const uint32_t nk = (p.K + BK - 1) / BK;  // >= 1: an empty K takes the generic kernel
+  PipeWalk w;
+  w.start(p, BK);
+  const uint32_t lds0_addr = lds_address(lds0);
+  const uint32_t lds1_addr = lds_address(lds1);
+  auto copy = [&](int q, uint32_t stage) {
+    if (q < CopyA::NI) ca.issue_one(q, static_cast<const S*>(p.a) + w.oa, stage);
+    else cb.issue_one(q - CopyA::NI, static_cast<const S*>(p.b) + w.ob, stage + uint32_t(BM * BK * sizeof(S)));
+  };
+#pragma unroll
+  for (int q = 0; q < NCOPY; ++q) copy(q, lds0_addr);
+  w.advance(p, nk, BK);
+#pragma unroll
+  for (int q = 0; q < NCOPY; ++q) copy(q, lds1_addr);
+  w.advance(p, nk, BK);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY) : "memory");  // K tile 0 of this wave landed
+  __syncthreads();
+  frags(lds0, 0, 0);
+
+  // first: the tile's first K tile, whose first MFMAs start the accumulators from 0
+  auto step = [&](S* stage_cur, const S* stage_nxt, uint32_t cur_addr, auto first) {
+    // substep 0: its MFMAs interleaved with the fragment reads of substep 1
+    frags(stage_cur, 1, 1);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (decltype(first)::value) Mma16<T>::mma_first(acc[i][j], bf[0][j], af[0][i]);
+        else Mma16<T>::mma(acc[i][j], bf[0][j], af[0][i]);
+      }
+#pragma unroll
+    for (int q = 0; q < MMAS; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                    // one MFMA
+      if (q < FM + FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // K tile kt+1 complete for everyone; every read of stage kt done
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    // substep 1: its MFMAs, the copies of K tile kt+2 into this stage and the first
+    // fragments of K tile kt+1, interleaved in program order
+#pragma unroll
+    for (int q = 0; q < MMAS; ++q) {
+      Mma16<T>::mma(acc[q / FN][q % FN], bf[1][q % FN], af[1][q / FN]);
+      if (q < NCOPY) copy(q, cur_addr);
+      if (q < FM) af[0][q] = *reinterpret_cast<const uint4*>(stage_nxt + abase + kofs[0] + q * 16 * BK);
+      else if (q < FM + FN)
+        bf[0][q - FM] = *reinterpret_cast<const uint4*>(stage_nxt + bbase + kofs[0] + (q - FM) * 16 * BK);
+    }
+    w.advance(p, nk, BK);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  using First = std::integral_constant<bool, true>;
+  using Next = std::integral_constant<bool, false>;
+  step(lds0, lds1, lds0_addr, First{});
+  uint32_t kt = 1;
+  for (; kt + 1 < nk; kt += 2) {
+    step(lds1, lds0, lds1_addr, Next{});
+    step(lds0, lds1, lds0_addr, Next{});
+  }
+  if (kt < nk) step(lds1, lds0, lds1_addr, Next{});
+  pipe16_drain(acc);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  store_tile16<T, BN, FM, FN>(p, lds0, acc, m0, n0, boff_c);
+}
+
 // ---- launcher ----------------------------------------------------------------------
 template <typename T, int BM, int BN, int WM, int WN, int LA, int LB, int PF>
 int launch_one(const ContractArgs& p, hipStream_t s, const char* name) {
@@ -855,8 +1119,13 @@ int launch_layouts(const ContractArgs& p, int la, int lb, hipStream_t s, const c
   if (la == kKContig && lb == kKContig) {
     if constexpr (BM == 256 && BN == 256 && sizeof(typename Traits<T>::S) == 2) {
       if (!p.off32) return launch_one<T, BM, BN, WM, WN, kKContig, kKContig, PF>(p, s, name);
-      contract_pipe<T><<<p.total_tiles, 256, 0, s>>>(p);
-      set_kernel("contract_pipe_256x256");
+      if (p.pipe_bn == 224) {
+        contract_pipe16<T, 224><<<p.total_tiles, 256, 0, s>>>(p);
+        set_kernel("contract_pipe16_256x224");
+      } else {
+        contract_pipe<T><<<p.total_tiles, 256, 0, s>>>(p);
+        set_kernel("contract_pipe_256x256");
+      }
       return check_launch("es_contract");
     }
     return launch_one<T, BM, BN, WM, WN, kKContig, kKContig, PF>(p, s, name);
