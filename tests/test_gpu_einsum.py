@@ -301,18 +301,18 @@ def test_repeated_calls_replay_with_fresh_data_and_geometry(gpu):
         # an odd (3) and an even (4) number of 64-deep K tiles.  Both of these cut into
         # two rounds of one tile per CU with 256 x 224 tiles as with 256 x 256 ones,
         # so the narrower tiles are chosen.
-        ("m k, n k -> m n", [(4136, 192), (4072, 192)], "contract_pipe16_256x224"),
-        ("m k, n k -> m n", [(4096, 256), (4200, 256)], "contract_pipe16_256x224"),
+        ("m k, n k -> m n", [(4136, 192), (4072, 192)], "contract_pipe_256x224"),
+        ("m k, n k -> m n", [(4096, 256), (4200, 256)], "contract_pipe_256x224"),
         # config 4's shape (N = 1792 = 8 x 224), and a ragged N edge inside a 224 tile
-        ("b n c, h c -> b n h", [(8, 2048, 128), (1792, 128)], "contract_pipe16_256x224"),
-        ("m k, n k -> m n", [(16384, 192), (1700, 192)], "contract_pipe16_256x224"),
+        ("b n c, h c -> b n h", [(8, 2048, 128), (1792, 128)], "contract_pipe_256x224"),
+        ("m k, n k -> m n", [(16384, 192), (1700, 192)], "contract_pipe_256x224"),
         # two K sub-axes (the inner one exactly one K tile), batch offsets
         ("m a k, n a k -> m n", [(4096, 3, 64), (4096, 3, 64)], "contract_pipe_256x256"),
         ("b m k, b n k -> b m n", [(16, 1024, 128), (16, 1000, 128)], "contract_pipe_256x256"),
         # an M-contiguous operand: copied K-contiguous first, then the pipelined kernel
         ("k m, n k -> m n", [(128, 4096), (4096, 128)], "contract_pipe_256x256"),
         # both operands contiguous along M / N (the C2 pattern on both sides)
-        ("k m, k n -> m n", [(192, 4096), (192, 4136)], "contract_pipe16_256x224"),
+        ("k m, k n -> m n", [(192, 4096), (192, 4136)], "contract_pipe_256x224"),
     ],
 )
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -337,7 +337,7 @@ def test_large_tiles_f32_m_contiguous(gpu):
     [
         (4096, 4096, 64, "contract_pipe_256x256"),
         (4096, 4096, 128, "contract_pipe_256x256"),
-        (16384, 1792, 64, "contract_pipe16_256x224"),
+        (16384, 1792, 64, "contract_pipe_256x224"),
         (96, 80, 1, None),
     ],
 )

@@ -11,25 +11,27 @@
 // 16-byte chunk c of row r stored at chunk position c ^ ((r / 2) % 8), so fragment
 // reads (32 consecutive rows, one chunk) and tile writes are free of bank conflicts.
 // A 16-byte ds_read gives a lane one MFMA fragment:
-//   * bf16/f16: v_mfma_f32_32x32x16 — lane l holds k = 8*(l/32) .. +7 of row l%32;
-//   * f32:      v_mfma_f32_32x32x2  — a 16-byte read gives a lane 4 consecutive
-//     k; four MFMAs consume them, lanes 0-31 supplying k 0..3 and lanes 32-63
-//     k 4..7.  Both operands use the same k assignment, so every product
+//   * contract_pipe, bf16/f16: v_mfma_f32_16x16x32 — lane l holds k = 8*(l/16) .. +7
+//     of row l%16;
+//   * contract_kernel, bf16/f16: v_mfma_f32_32x32x16 — lane l holds k = 8*(l/32) .. +7
+//     of row l%32;
+//   * contract_kernel, f32: v_mfma_f32_32x32x2 — a 16-byte read gives a lane 4
+//     consecutive k; four MFMAs consume them, lanes 0-31 supplying k 0..3 and lanes
+//     32-63 k 4..7.  Both operands use the same k assignment, so every product
 //     A[m,k]*B[n,k] is formed exactly once (only the summation order differs).
 // The MFMA's first operand is the N-side fragment and the second the M-side
 // one, so the accumulator holds C^T: each lane ends with 4 consecutive n of
 // one m.  The epilogue computes every tile row's and column's output offset once
 // into LDS tables, stages 32-row slices of the tile in LDS and writes them with
-// 16-byte stores along n when n is the output's contiguous axis.
+// 16-byte streaming stores along n when n is the output's contiguous axis.
 //
 // Kernels:
-//   * contract_pipe (16-bit types, both operands K-contiguous, 256 x 256 tiles):
-//     4 waves of 128 x 128, two LDS stages filled by global_load_lds_dwordx4
-//     copies issued a full K tile ahead, an explicit MFMA / LDS-read / copy
-//     interleave (see es_contract_kernel.h);
-//   * contract_pipe16 (the same operands, 256 x 224 tiles): the pipeline on
-//     v_mfma_f32_16x16x32 with waves of 128 x 112, chosen when an N extent cuts into
-//     fewer rounds of one tile per CU than with 256-wide tiles (N = 1792);
+//   * contract_pipe (16-bit types, both operands K-contiguous, 256 x 256 or 256 x 224
+//     tiles): 4 waves of 128 x 128 (or 128 x 112), two LDS stages filled by
+//     global_load_lds_dwordx4 copies issued a full K tile ahead, an explicit MFMA /
+//     LDS-read / copy interleave (see es_contract_kernel.h).  224-wide tiles are chosen
+//     when an N extent cuts into fewer rounds of one tile per CU than with 256-wide
+//     ones (N = 1792);
 //   * contract_kernel (every other case): WM x WN waves over a BM x BN tile,
 //     double-buffered LDS with one barrier per K tile.  Its loaders:
 //       - K-contiguous: direct global -> LDS copies;
@@ -61,7 +63,7 @@ struct ContractArgs {
   uint32_t tiles_m, tiles_n;
   uint32_t group_n;      // N-tiles per tile group (divides tiles_n; see tile_of)
   uint32_t total_tiles;
-  uint32_t pipe_bn;      // 224: the 256 x 224 tiles of contract_pipe16; 0 otherwise
+  uint32_t pipe_bn;      // 224: contract_pipe's 256 x 224 tiles; 0: 256 x 256
   int32_t vstore;        // 16-byte vector stores along n
   int32_t off32;         // every byte offset into A and B fits in 32 bits
   uint32_t k_inner;      // extent of the innermost K sub-axis (fast paths: a multiple of BK)

@@ -166,7 +166,7 @@ extern "C" int es_contract(const es_contract_desc* d, const void* a, const void*
   const uint64_t t = uint64_t(tile_of[config]);
   const uint64_t tm = (nm + t - 1) / t;
   uint64_t tn = (nn + t - 1) / t;
-  // 256 x 224 tiles (contract_pipe16) when they take fewer rounds of one tile per CU;
+  // 256 x 224 tiles (contract_pipe) when they take fewer rounds of one tile per CU;
   // a 224-wide tile does 7/8 of the work of a 256-wide one, and its narrower waves read
   // a little more LDS per flop (charged as 5 %)
   p.pipe_bn = 0;

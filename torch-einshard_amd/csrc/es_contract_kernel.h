@@ -616,19 +616,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const Contrac
   store_tile<T, BM, BN, WM, WN>(p, lds, acc, m0, n0, boff_c);
 }
 
-// ---- software-pipelined 256 x 256 kernel, both operands K-contiguous ------------
-// Four waves (2 x 2), each owning a 128 x 128 block: per 16-deep k step a wave reads
-// 8 fragments for 16 MFMAs, half the LDS reads per MFMA of the 8-wave kernel.  With
-// one wave per SIMD nothing hides a stall, so the schedule is explicit:
-//   substeps 0 .. NS-2: 16 MFMAs interleaved with the fragment reads of the next
-//                       substep;
-//   barrier:            the K tile for step kt+1 has landed (own copies: vmcnt(0);
-//                       everyone's: the barrier) and nobody reads stage kt any more;
-//   substep NS-1:       16 MFMAs interleaved with the copies of K tile kt+2 into
-//                       stage kt (issued a full step before they are needed) and the
-//                       fragment reads of step kt+1's first substep.
-// The loop body has no branches: past the last tile the copies re-fetch the last tile
-// into a stage nobody reads.
+// ---- software-pipelined kernel, both operands K-contiguous (pieces) ----------------
+// K walk of contract_pipe's copies.  The loop body has no branches: past the last K
+// tile the copies re-fetch the last tile into a stage nobody reads.
 struct PipeWalk {
   uint32_t t;     // K tile index of the next copy
   uint32_t kin;   // position inside the innermost K sub-axis
@@ -702,173 +692,38 @@ struct PipeCopies {
   }
 };
 
-template <typename T>
-__global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
-  using S = typename Traits<T>::S;
-  constexpr int BM = 256, BN = 256, WM = 2, WN = 2, NT = 256;
-  constexpr int VEC = Traits<T>::VEC;
-  constexpr int BK = kRowBytes / int(sizeof(S));
-  constexpr int KSTEP = 2 * VEC;
-  constexpr int NS = BK / KSTEP;
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int STAGE = (BM + BN) * BK;
-  constexpr int MMA_PER_FRAG = sizeof(S) == 4 ? 4 : 1;  // MFMA instructions per fragment pair
-  constexpr int MMAS = FM * FN * MMA_PER_FRAG;          // per substep
-  using CopyA = PipeCopies<S, BM, WM * WN, 0>;
-  using CopyB = PipeCopies<S, BN, WM * WN, 1>;
-  constexpr int NCOPY = CopyA::NI + CopyB::NI;  // copies per wave per K tile
-  static_assert(NS % 2 == 0, "fragment double buffer alternates within a step");
-  static_assert(epilogue_bytes<S, BM, BN, WM>() <= int(sizeof(S)) * STAGE, "epilogue must fit in one stage");
-  static_assert(WTM % 16 == 0 && WTN % 16 == 0, "fragment rows of a lane share one swizzle key");
-
-  // two stages as two arrays: the compiler can then tell the copies into one from
-  // the fragment reads of the other and does not wait for the copies before reading
-  __shared__ __attribute__((aligned(1024))) S lds0[STAGE];
-  __shared__ __attribute__((aligned(1024))) S lds1[STAGE];
-
-  const int tid = threadIdx.x;
-  const int lane = tid % 64;
-  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
-  const int wm = wave / WN;
-  const int wn = wave % WN;
-
-  uint32_t bidx, tm, tn;
-  tile_of(p, blockIdx.x, bidx, tm, tn);
-  const uint32_t m0 = tm * BM;
-  const uint32_t n0 = tn * BN;
-  const int64_t boff_a = group_offset<0>(p.gb, bidx);
-  const int64_t boff_b = group_offset<1>(p.gb, bidx);
-  const int64_t boff_c = group_offset<2>(p.gb, bidx);
-
-  CopyA ca;
-  CopyB cb;
-  ca.init(p, wave, lane, m0, boff_a);
-  cb.init(p, wave, lane, n0, boff_b);
-
-  f32x16 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  // Fragment addressing.  Fragment rows of this lane are lane % 32 plus multiples of
-  // 16, so they share the swizzle key ((row / 2) % 8): the chunk position of k-chunk
-  // 2 * ks + lane / 32 is the same for all of them, and a fragment's address is a
-  // per-substep lane offset plus a compile-time row offset.
-  const int lrow = lane % 32;
-  int kofs[NS];
-#pragma unroll
-  for (int ks = 0; ks < NS; ++ks) kofs[ks] = lrow * BK + swz(lrow, ks * 2 + lane / 32) * VEC;
-  const int abase = wm * WTM * BK;
-  const int bbase = BM * BK + wn * WTN * BK;
-
-  uint4 af[2][FM], bf[2][FN];
-  auto frags = [&](const S* stage, int buf, int ks) {
-    const S* a = stage + abase + kofs[ks];
-    const S* b = stage + bbase + kofs[ks];
-#pragma unroll
-    for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const uint4*>(a + i * 32 * BK);
-#pragma unroll
-    for (int j = 0; j < FN; ++j) bf[buf][j] = *reinterpret_cast<const uint4*>(b + j * 32 * BK);
-  };
-  auto mmas = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) Traits<T>::mma(acc[i][j], bf[buf][j], af[buf][i]);
-  };
-
-  const uint32_t nk = (p.K + BK - 1) / BK;  // >= 1: an empty K takes the generic kernel
-  PipeWalk w;
-  w.start(p, BK);
-  const uint32_t lds0_addr = lds_address(lds0);
-  const uint32_t lds1_addr = lds_address(lds1);
-  // copy q (0 .. NCOPY-1) of the tile the walk points at into the stage at `stage`
-  auto copy = [&](int q, uint32_t stage) {
-    if (q < CopyA::NI) ca.issue_one(q, static_cast<const S*>(p.a) + w.oa, stage);
-    else cb.issue_one(q - CopyA::NI, static_cast<const S*>(p.b) + w.ob, stage + uint32_t(BM * BK * sizeof(S)));
-  };
-#pragma unroll
-  for (int q = 0; q < NCOPY; ++q) copy(q, lds0_addr);
-  w.advance(p, nk, BK);
-#pragma unroll
-  for (int q = 0; q < NCOPY; ++q) copy(q, lds1_addr);
-  w.advance(p, nk, BK);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY) : "memory");  // tile 0 of this wave landed
-  __syncthreads();
-  frags(lds0, 0, 0);
-
-  // one K tile: stage_cur holds it, stage_nxt the next one
-  auto step = [&](S* stage_cur, const S* stage_nxt, uint32_t cur_addr) {
-#pragma unroll
-    for (int ks = 0; ks + 1 < NS; ++ks) {
-      frags(stage_cur, (ks + 1) & 1, ks + 1);
-      mmas(ks & 1);
-#pragma unroll
-      for (int q = 0; q < MMAS; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                    // one MFMA
-        if (q < FM + FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-      }
-      __builtin_amdgcn_sched_barrier(0);  // substeps are scheduled one at a time
-    }
-    // tile kt+1 complete for everyone; every read of stage kt done
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    // last substep: its MFMAs, the copies of tile kt+2 into this stage and the first
-    // fragments of tile kt+1, interleaved in program order
-    {
-      constexpr int buf = (NS - 1) & 1;
-#pragma unroll
-      for (int q = 0; q < FM * FN; ++q) {
-        Traits<T>::mma(acc[q / FN][q % FN], bf[buf][q % FN], af[buf][q / FN]);
-        if (q < NCOPY) copy(q, cur_addr);
-        if (q < FM) af[0][q] = *reinterpret_cast<const uint4*>(stage_nxt + abase + kofs[0] + q * 32 * BK);
-        else if (q < FM + FN) bf[0][q - FM] = *reinterpret_cast<const uint4*>(stage_nxt + bbase + kofs[0] + (q - FM) * 32 * BK);
-      }
-#pragma unroll
-      for (int q = FM * FN; q < NCOPY; ++q) copy(q, cur_addr);
-      w.advance(p, nk, BK);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  uint32_t kt = 0;
-  for (; kt + 1 < nk; kt += 2) {
-    step(lds0, lds1, lds0_addr);
-    step(lds1, lds0, lds1_addr);
-  }
-  if (kt < nk) step(lds0, lds1, lds0_addr);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  store_tile<T, BM, BN, WM, WN>(p, lds0, acc, m0, n0, boff_c);
-}
-
-// ---- 16x16x32 pipelined kernel: 256 x BN tiles, BN = 256 or 224 ---------------------
-// The pipeline of contract_pipe on v_mfma_f32_16x16x32_{bf16,f16}: four waves (2 x 2)
-// each own 128 x BN/2 as 8 x BN/32 blocks of 16 x 16, and a 64-deep K tile is two
-// substeps of 32.  Blocks of 16 allow BN = 224 (waves of 128 x 112): an N extent of
-// 7 x 256 = 1792 (one tensor-parallel rank's share of a 14336-wide weight) then cuts
-// into 8 tiles instead of 7, and 16384 x 1792 into 512 tiles, two whole rounds of one
-// tile per CU, where 256 x 256 tiles leave a quarter of the CUs idle in the second.
+// ---- software-pipelined kernel: 256 x BN tiles (BN = 256 or 224), 16-bit types -------
+// Four waves (2 x 2) each own 128 x BN/2 as 8 x BN/32 blocks of 16 x 16 on
+// v_mfma_f32_16x16x32_{bf16,f16}; a 64-deep K tile is two substeps of 32 k.  Two LDS
+// stages, filled by global_load_lds_dwordx4 copies issued a full K tile ahead.  With one
+// wave per SIMD nothing hides a stall, so the schedule is explicit:
+//   substep 0: its MFMAs, with the fragment reads of substep 1 spread evenly over them;
+//   barrier:   K tile kt+1 has landed (own copies: vmcnt(0); everyone's: the barrier)
+//              and nobody reads stage kt any more;
+//   substep 1: its MFMAs, with the copies of K tile kt+2 into stage kt and the fragment
+//              reads of K tile kt+1's first substep spread evenly over them (bunching
+//              them measured 24 % slower: the copies and reads then queue on LDS).
+// Blocks of 16 allow BN = 224 (waves of 128 x 112): an N extent of 7 x 256 = 1792 (one
+// tensor-parallel rank's share of a 14336-wide weight) then cuts into 8 tiles instead of
+// 7, and 16384 x 1792 into 512 tiles, two whole rounds of one tile per CU, where 256 x 256
+// tiles leave a quarter of the CUs idle in the second.
 // Lane l of a fragment read holds k = 8 * (l / 16) .. +7 of row l % 16 (one 16-byte LDS
 // read); the first MFMA operand is the N-side fragment, so the accumulator holds C^T and
 // lane l ends with 4 consecutive n (4 * (l / 16) + 0..3) of m = l % 16.
-// MFMAs of contract_pipe16 as inline assembly with the accumulator tied to the result
+// MFMAs of contract_pipe as inline assembly with the accumulator tied to the result
 // ("+a": read and written in place, in AGPRs).  The builtin is selected in a form
 // whose result need not share the accumulator's registers, and with 56 accumulators
 // per wave the register allocator then rotated them through the AGPRs with a copy per
-// accumulator per K tile (measured 40 % slower).  The compiler cannot see hazards across
+// accumulator per K tile (measured 40 % slower than tied).  The compiler cannot see hazards across
 // inline assembly, so the kernel avoids them by construction: nothing but these MFMAs
 // writes the accumulators (the first MFMA of a tile takes the constant 0 as its
 // accumulator, mma_first), the fragment operands come straight from LDS reads, and
-// pipe16_drain separates the last MFMA from the first VALU read of a result.
+// pipe_drain separates the last MFMA from the first VALU read of a result.
 template <typename T>
-struct Mma16;
+struct PipeMma;
 
 template <>
-struct Mma16<bf16_t> {
+struct PipeMma<bf16_t> {
   static __device__ __forceinline__ void mma(f32x4& acc, const uint4& nfrag, const uint4& mfrag) {
     asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
                  : "+a"(acc)
@@ -882,7 +737,7 @@ struct Mma16<bf16_t> {
 };
 
 template <>
-struct Mma16<f16_t> {
+struct PipeMma<f16_t> {
   static __device__ __forceinline__ void mma(f32x4& acc, const uint4& nfrag, const uint4& mfrag) {
     asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"
                  : "+a"(acc)
@@ -899,7 +754,7 @@ struct Mma16<f16_t> {
 // before a VALU read), then every accumulator passes through an empty statement that
 // follows them, so no read of a result can be scheduled before the wait.
 template <int FM, int FN>
-__device__ __forceinline__ void pipe16_drain(f32x4 (&acc)[FM][FN]) {
+__device__ __forceinline__ void pipe_drain(f32x4 (&acc)[FM][FN]) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -907,13 +762,13 @@ __device__ __forceinline__ void pipe16_drain(f32x4 (&acc)[FM][FN]) {
     for (int j = 0; j < FN; ++j) asm volatile("" : "+a"(acc[i][j]));
 }
 
-// Epilogue of contract_pipe16: eight passes of 32 tile rows.  Pass q stages rows
+// Epilogue of contract_pipe: eight passes of 32 tile rows.  Pass q stages rows
 // wm * 128 + 32 * (q % 4) + 0..31 (wm = q / 4), written by the two waves of wave row wm
 // as [row][n] in `lds`, then the whole work-group writes them out (16-byte streaming
 // stores along n when n is the output's contiguous axis, element stores otherwise).
 // The caller has drained every copy into LDS and synchronised the work-group.
 template <typename T, int BN, int FM, int FN>
-__device__ __forceinline__ void store_tile16(const ContractArgs& p, void* lds, const f32x4 (&acc)[FM][FN], uint32_t m0,
+__device__ __forceinline__ void store_pipe(const ContractArgs& p, void* lds, const f32x4 (&acc)[FM][FN], uint32_t m0,
                                              uint32_t n0, int64_t boff_c) {
   using S = typename Traits<T>::S;
   constexpr int BM = 256, WTM = 128, WTN = BN / 2, VEC = 8, NT = 256;
@@ -979,7 +834,7 @@ __device__ __forceinline__ void store_tile16(const ContractArgs& p, void* lds, c
 }
 
 template <typename T, int BN>
-__global__ __launch_bounds__(256, 1) void contract_pipe16(const ContractArgs p) {
+__global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   using S = typename Traits<T>::S;
   constexpr int BM = 256, WM = 2, WN = 2;
   constexpr int VEC = 8;
@@ -1066,13 +921,14 @@ __global__ __launch_bounds__(256, 1) void contract_pipe16(const ContractArgs p) 
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        if constexpr (decltype(first)::value) Mma16<T>::mma_first(acc[i][j], bf[0][j], af[0][i]);
-        else Mma16<T>::mma(acc[i][j], bf[0][j], af[0][i]);
+        if constexpr (decltype(first)::value) PipeMma<T>::mma_first(acc[i][j], bf[0][j], af[0][i]);
+        else PipeMma<T>::mma(acc[i][j], bf[0][j], af[0][i]);
       }
 #pragma unroll
     for (int q = 0; q < MMAS; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                    // one MFMA
-      if (q < FM + FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      // the fragment reads spread evenly over the substep
+      if ((q * (FM + FN)) / MMAS != ((q + 1) * (FM + FN)) / MMAS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     // K tile kt+1 complete for everyone; every read of stage kt done
@@ -1082,11 +938,15 @@ __global__ __launch_bounds__(256, 1) void contract_pipe16(const ContractArgs p) 
     // fragments of K tile kt+1, interleaved in program order
 #pragma unroll
     for (int q = 0; q < MMAS; ++q) {
-      Mma16<T>::mma(acc[q / FN][q % FN], bf[1][q % FN], af[1][q / FN]);
-      if (q < NCOPY) copy(q, cur_addr);
-      if (q < FM) af[0][q] = *reinterpret_cast<const uint4*>(stage_nxt + abase + kofs[0] + q * 16 * BK);
-      else if (q < FM + FN)
-        bf[0][q - FM] = *reinterpret_cast<const uint4*>(stage_nxt + bbase + kofs[0] + (q - FM) * 16 * BK);
+      PipeMma<T>::mma(acc[q / FN][q % FN], bf[1][q % FN], af[1][q / FN]);
+      // copies and fragment reads spread evenly over the substep, alternating
+      const int c0 = (q * NCOPY) / MMAS, c1 = ((q + 1) * NCOPY) / MMAS;
+      if (c0 != c1) copy(c0, cur_addr);
+      const int r0 = (q * (FM + FN)) / MMAS, r1 = ((q + 1) * (FM + FN)) / MMAS;
+      if (r0 != r1) {
+        if (r0 < FM) af[0][r0] = *reinterpret_cast<const uint4*>(stage_nxt + abase + kofs[0] + r0 * 16 * BK);
+        else bf[0][r0 - FM] = *reinterpret_cast<const uint4*>(stage_nxt + bbase + kofs[0] + (r0 - FM) * 16 * BK);
+      }
     }
     w.advance(p, nk, BK);
     __builtin_amdgcn_sched_barrier(0);
@@ -1100,10 +960,10 @@ __global__ __launch_bounds__(256, 1) void contract_pipe16(const ContractArgs p) 
     step(lds0, lds1, lds0_addr, Next{});
   }
   if (kt < nk) step(lds1, lds0, lds1_addr, Next{});
-  pipe16_drain(acc);
+  pipe_drain(acc);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  store_tile16<T, BN, FM, FN>(p, lds0, acc, m0, n0, boff_c);
+  store_pipe<T, BN, FM, FN>(p, lds0, acc, m0, n0, boff_c);
 }
 
 // ---- launcher ----------------------------------------------------------------------
@@ -1120,10 +980,10 @@ int launch_layouts(const ContractArgs& p, int la, int lb, hipStream_t s, const c
     if constexpr (BM == 256 && BN == 256 && sizeof(typename Traits<T>::S) == 2) {
       if (!p.off32) return launch_one<T, BM, BN, WM, WN, kKContig, kKContig, PF>(p, s, name);
       if (p.pipe_bn == 224) {
-        contract_pipe16<T, 224><<<p.total_tiles, 256, 0, s>>>(p);
-        set_kernel("contract_pipe16_256x224");
+        contract_pipe<T, 224><<<p.total_tiles, 256, 0, s>>>(p);
+        set_kernel("contract_pipe_256x224");
       } else {
-        contract_pipe<T><<<p.total_tiles, 256, 0, s>>>(p);
+        contract_pipe<T, 256><<<p.total_tiles, 256, 0, s>>>(p);
         set_kernel("contract_pipe_256x256");
       }
       return check_launch("es_contract");
