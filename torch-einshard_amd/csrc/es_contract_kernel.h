@@ -762,26 +762,34 @@ __device__ __forceinline__ void pipe_drain(f32x4 (&acc)[FM][FN]) {
     for (int j = 0; j < FN; ++j) asm volatile("" : "+a"(acc[i][j]));
 }
 
-// Epilogue of contract_pipe: eight passes of 32 tile rows.  Pass q stages rows
-// wm * 128 + 32 * (q % 4) + 0..31 (wm = q / 4), written by the two waves of wave row wm
-// as [row][n] in `lds`, then the whole work-group writes them out (16-byte streaming
-// stores along n when n is the output's contiguous axis, element stores otherwise).
-// The caller has drained every copy into LDS and synchronised the work-group.
+// Epilogue of contract_pipe.  The tile is staged in the two (now free) LDS stages,
+// wave row 0's rows in stage 0 and wave row 1's in stage 1, in as few passes as fit
+// with the row / column offset tables beside them: one pass for 256 x 224 tiles, two of
+// 128 rows for 256 x 256.  All four waves stage their accumulators, one barrier, then
+// the whole work-group writes the rows out (16-byte streaming stores along n when n is
+// the output's contiguous axis, element stores otherwise).  The caller has drained
+// every copy into LDS and synchronised the work-group.
 template <typename T, int BN, int FM, int FN>
-__device__ __forceinline__ void store_pipe(const ContractArgs& p, void* lds, const f32x4 (&acc)[FM][FN], uint32_t m0,
-                                             uint32_t n0, int64_t boff_c) {
+__device__ __forceinline__ void store_pipe(const ContractArgs& p, typename Traits<T>::S* lds0,
+                                           typename Traits<T>::S* lds1, const f32x4 (&acc)[FM][FN], uint32_t m0,
+                                           uint32_t n0, int64_t boff_c) {
   using S = typename Traits<T>::S;
-  constexpr int BM = 256, WTM = 128, WTN = BN / 2, VEC = 8, NT = 256;
-  constexpr int SROWS = 32;
+  constexpr int BM = 256, WTN = BN / 2, VEC = 8, NT = 256;
   constexpr int SLD = BN + VEC;  // staging row pitch (elements)
-  S* stage = static_cast<S*>(lds);
-  int64_t* row_off = reinterpret_cast<int64_t*>(static_cast<char*>(lds) + SROWS * SLD * int(sizeof(S)));
-  int64_t* col_off = row_off + BM;
+  constexpr int STAGE_BYTES = (BM + BN) * kRowBytes;
+  constexpr int TABLES = BM * 8;  // the larger table (rows)
+  constexpr int P = (16 * FM) * SLD * int(sizeof(S)) + TABLES <= STAGE_BYTES ? 1 : 2;  // passes
+  constexpr int BPP = FM / P;   // 16-row blocks per wave row per pass
+  constexpr int RR = 16 * BPP;  // rows per stage per pass
+  static_assert(FM % P == 0 && RR * SLD * int(sizeof(S)) + TABLES <= STAGE_BYTES, "epilogue fits the stages");
+  int64_t* row_off = reinterpret_cast<int64_t*>(reinterpret_cast<char*>(lds0) + RR * SLD * int(sizeof(S)));
+  int64_t* col_off = reinterpret_cast<int64_t*>(reinterpret_cast<char*>(lds1) + RR * SLD * int(sizeof(S)));
   const int tid = threadIdx.x;
   const int lane = tid % 64;
   const int wave = tid / 64;
   const int wm = wave / 2;
   const int wn = wave % 2;
+  S* region = wm == 0 ? lds0 : lds1;
   S* C = static_cast<S*>(p.c);
   const KArgs kp = kernel_args();
   for (int r = tid; r < BM; r += NT) {
@@ -793,43 +801,43 @@ __device__ __forceinline__ void store_pipe(const ContractArgs& p, void* lds, con
     col_off[c] = n < p.N ? group_offset_k<2>(&kp->gn, n) : -1;
   }
 #pragma unroll
-  for (int q = 0; q < 2 * FM / 2; ++q) {
-    const int pw = q / (FM / 2);
-    const int i0 = 2 * (q % (FM / 2));
-    if (wm == pw) {
+  for (int q = 0; q < P; ++q) {
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii)
+    for (int ii = 0; ii < BPP; ++ii)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const f32x4& a = acc[i0 + ii][j];
-          *reinterpret_cast<uint2*>(stage + (ii * 16 + lane % 16) * SLD + wn * WTN + j * 16 + 4 * (lane / 16)) =
-              uint2{Traits<T>::pack2(a[0], a[1]), Traits<T>::pack2(a[2], a[3])};
-        }
-    }
+      for (int j = 0; j < FN; ++j) {
+        const f32x4& a = acc[q * BPP + ii][j];
+        *reinterpret_cast<uint2*>(region + (ii * 16 + lane % 16) * SLD + wn * WTN + j * 16 + 4 * (lane / 16)) =
+            uint2{Traits<T>::pack2(a[0], a[1]), Traits<T>::pack2(a[2], a[3])};
+      }
     lds_barrier();
-    const int row0 = pw * WTM + i0 * 16;  // tile row of staged row 0
+    // staged row rr of stage h is tile row h * 128 + q * RR + rr
     if (p.vstore) {
-      constexpr int CV = BN / VEC;  // vectors per staged row
-      for (int v = tid; v < SROWS * CV; v += NT) {
-        const int r = v / CV;
-        const int cv = v - r * CV;
-        const int64_t ro = row_off[row0 + r];
+      constexpr int CV = BN / VEC;  // vectors per row
+      for (int v = tid; v < 2 * RR * CV; v += NT) {
+        const int h = v / (RR * CV);
+        const int rem = v - h * (RR * CV);
+        const int rr = rem / CV;
+        const int cv = rem - rr * CV;
+        const int64_t ro = row_off[h * 128 + q * RR + rr];
         const int64_t co = col_off[cv * VEC];
         // nontemporal: the output is not read again by this kernel, so it is not kept in L2
         if (ro >= 0 && co >= 0)
-          __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(stage + r * SLD + cv * VEC),
+          __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>((h ? lds1 : lds0) + rr * SLD + cv * VEC),
                                       reinterpret_cast<u32x4*>(C + ro + co));
       }
     } else {
-      for (int v = tid; v < SROWS * BN; v += NT) {
-        const int r = v / BN;
-        const int cn = v - r * BN;
-        const int64_t ro = row_off[row0 + r];
+      for (int v = tid; v < 2 * RR * BN; v += NT) {
+        const int h = v / (RR * BN);
+        const int rem = v - h * (RR * BN);
+        const int rr = rem / BN;
+        const int cn = rem - rr * BN;
+        const int64_t ro = row_off[h * 128 + q * RR + rr];
         const int64_t co = col_off[cn];
-        if (ro >= 0 && co >= 0) C[ro + co] = stage[r * SLD + cn];
+        if (ro >= 0 && co >= 0) C[ro + co] = (h ? lds1 : lds0)[rr * SLD + cn];
       }
     }
-    lds_barrier();
+    if (q + 1 < P) lds_barrier();
   }
 }
 
@@ -850,7 +858,6 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   static_assert(sizeof(S) == 2 && NS == 2, "16-bit element types, two substeps per K tile");
   static_assert(WTN % 16 == 0 && FM % 2 == 0, "tile shape");
   static_assert(NCOPY <= MMAS && FM + FN <= MMAS, "last substep interleave");
-  static_assert(32 * (BN + VEC) * int(sizeof(S)) + (BM + BN) * 8 <= int(sizeof(S)) * STAGE, "epilogue fits a stage");
 
   __shared__ __attribute__((aligned(1024))) S lds0[STAGE];
   __shared__ __attribute__((aligned(1024))) S lds1[STAGE];
@@ -963,7 +970,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   pipe_drain(acc);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  store_pipe<T, BN, FM, FN>(p, lds0, acc, m0, n0, boff_c);
+  store_pipe<T, BN, FM, FN>(p, lds0, lds1, acc, m0, n0, boff_c);
 }
 
 // ---- launcher ----------------------------------------------------------------------
