@@ -147,6 +147,15 @@ typedef struct {
 /* Replaces: torch.einsum binary with contracted labels (einsum.py:132 -> bmm). */
 int es_contract(const es_contract_desc* desc, const void* a, const void* b, void* c, void* stream);
 
+/* es_contract plus a bias: C[batch, m, n] = sum_k A * B + bias[n], with n the linear
+ * index over the N group and bias a dense vector of N elements of the descriptor's
+ * dtype, added in fp32 before the one rounding of the result.
+ * Replaces: the convolution with bias inside einconv (conv.py:195,
+ * F.conv{1,2,3}d(x, weight, bias, padding=0, dilation=...)), which einconv runs as a
+ * contraction over an overlapping strided view of the padded input (no im2col). */
+int es_contract_bias(const es_contract_desc* desc, const void* a, const void* b, const void* bias, void* c,
+                     void* stream);
+
 /* ---- library --------------------------------------------------------------- */
 int es_abi_version(void);
 const char* es_version(void);

@@ -22,7 +22,15 @@ def declared_entry_points():
 
 def test_header_declares_the_entry_points():
     names = declared_entry_points()
-    for required in ("es_gather", "es_bcast", "es_reduce", "es_reduce_workspace_bytes", "es_contract", "es_last_error"):
+    for required in (
+        "es_gather",
+        "es_bcast",
+        "es_reduce",
+        "es_reduce_workspace_bytes",
+        "es_contract",
+        "es_contract_bias",
+        "es_last_error",
+    ):
         assert required in names
 
 
@@ -62,6 +70,10 @@ def test_null_descriptor_is_rejected():
     assert status == _native.ES_ERR_INVALID and "null descriptor" in message
     status, message = _status("es_contract", None, None, None, None, None)
     assert status == _native.ES_ERR_INVALID
+    cdesc = _native.ContractDesc()
+    cdesc.dtype = 1
+    status, message = _status("es_contract_bias", ctypes.byref(cdesc), None, None, None, None, None)
+    assert status == _native.ES_ERR_INVALID and "null bias" in message
 
 
 def test_bad_descriptors_are_rejected_before_any_launch():

@@ -47,6 +47,8 @@ namespace es {
 
 enum OperandLayout { kKContig = 0, kMNContig = 1, kGeneric = 2 };
 
+constexpr int kKLevels = 4;  // K sub-axes the fast paths walk incrementally
+
 struct GroupArgs {
   int32_t n;
   FastDiv div[ES_MAX_AXES];
@@ -66,11 +68,16 @@ struct ContractArgs {
   uint32_t pipe_bn;      // 224: contract_pipe's 256 x 224 tiles; 0: 256 x 256
   int32_t vstore;        // 16-byte vector stores along n
   int32_t off32;         // every byte offset into A and B fits in 32 bits
-  uint32_t k_inner;      // extent of the innermost K sub-axis (fast paths: a multiple of BK)
   int64_t ka_inner;      // stride of the innermost K sub-axis in A
   int64_t kb_inner;      // ... in B
-  int64_t ka_outer;      // stride of the outer K sub-axis in A (fast paths have at most two)
-  int64_t kb_outer;      // ... in B
+  // Incremental K walk of the fast paths (at most kKLevels K sub-axes, the innermost a
+  // multiple of BK): level 0 counts K tiles inside the innermost sub-axis, level L > 0
+  // the L-th sub-axis out.  Advancing at level L (every level below it wrapping) adds
+  // kda[L] / kdb[L] to the tile's offset in A / B.
+  uint32_t kcnt[kKLevels];  // extent of each level (unused levels: never wrap)
+  int64_t kda[kKLevels];
+  int64_t kdb[kKLevels];
+  const void* bias;      // es_contract_bias: bias[n] added before rounding; else null
   GroupArgs gb, gm, gn, gk;
 };
 

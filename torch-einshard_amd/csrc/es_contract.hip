@@ -99,11 +99,39 @@ uint32_t group_width(uint64_t tiles_m, uint64_t tiles_n, uint64_t total) {
   return best;
 }
 
+// K walk levels (see ContractArgs::kcnt): level 0 = K tiles of the innermost sub-axis,
+// level L = the L-th sub-axis out; advancing at level L resets every level below it.
+void k_walk(const es_contract_desc* d, int bk, ContractArgs& p) {
+  for (int l = 0; l < kKLevels; ++l) {
+    p.kcnt[l] = 0xffffffffu;
+    p.kda[l] = p.kdb[l] = 0;
+  }
+  if (d->n_k == 0 || d->n_k > kKLevels) return;
+  const es_axis& in = d->k[d->n_k - 1];
+  const int64_t tiles = in.size / bk;
+  int64_t back_a = 0, back_b = 0;  // offset of the last position below the current level
+  p.kda[0] = int64_t(bk) * in.a;
+  p.kdb[0] = int64_t(bk) * in.b;
+  if (d->n_k > 1) p.kcnt[0] = uint32_t(tiles);
+  back_a = (tiles - 1) * int64_t(bk) * in.a;
+  back_b = (tiles - 1) * int64_t(bk) * in.b;
+  for (int l = 1; l < d->n_k; ++l) {
+    const es_axis& ax = d->k[d->n_k - 1 - l];
+    p.kda[l] = ax.a - back_a;
+    p.kdb[l] = ax.b - back_b;
+    if (l + 1 < d->n_k) p.kcnt[l] = uint32_t(ax.size);
+    back_a += (ax.size - 1) * ax.a;
+    back_b += (ax.size - 1) * ax.b;
+  }
+}
+
 }  // namespace
 }  // namespace es
 
-extern "C" int es_contract(const es_contract_desc* d, const void* a, const void* b, void* c, void* stream) {
-  using namespace es;
+namespace es {
+namespace {
+
+int contract(const es_contract_desc* d, const void* a, const void* b, const void* bias, void* c, void* stream) {
   if (d == nullptr) return fail(ES_ERR_INVALID, "es_contract: null descriptor");
   const int esz = dtype_size(d->dtype);
   if (esz == 0) return fail(ES_ERR_UNSUPPORTED, "es_contract: unsupported dtype");
@@ -136,11 +164,10 @@ extern "C" int es_contract(const es_contract_desc* d, const void* a, const void*
   p.batch = uint32_t(nb);
   p.ka_inner = d->n_k > 0 ? d->k[d->n_k - 1].a : 0;
   p.kb_inner = d->n_k > 0 ? d->k[d->n_k - 1].b : 0;
-  p.k_inner = d->n_k > 0 ? uint32_t(d->k[d->n_k - 1].size) : 0;
-  // the fast kernels walk K incrementally over at most two sub-axes
-  if (d->n_k > 2) la = lb = kGeneric;
-  p.ka_outer = d->n_k == 2 ? d->k[0].a : int64_t(p.k_inner) * p.ka_inner;
-  p.kb_outer = d->n_k == 2 ? d->k[0].b : int64_t(p.k_inner) * p.kb_inner;
+  p.bias = bias;
+  // the fast kernels walk K incrementally over at most kKLevels sub-axes
+  if (d->n_k > kKLevels) la = lb = kGeneric;
+  k_walk(d, bk, p);
   p.off32 = max_offset_bytes(d, 0, esz) + 16 < (uint64_t(1) << 32) && max_offset_bytes(d, 1, esz) + 16 < (uint64_t(1) << 32);
   p.vstore = 0;
   if (d->n_n > 0) {
@@ -193,4 +220,17 @@ extern "C" int es_contract(const es_contract_desc* d, const void* a, const void*
     case ES_F16: return launch_contract_f16(p, config, la, lb, s);
   }
   return fail(ES_ERR_UNSUPPORTED, "es_contract: unsupported dtype");
+}
+
+}  // namespace
+}  // namespace es
+
+extern "C" int es_contract(const es_contract_desc* d, const void* a, const void* b, void* c, void* stream) {
+  return es::contract(d, a, b, nullptr, c, stream);
+}
+
+extern "C" int es_contract_bias(const es_contract_desc* d, const void* a, const void* b, const void* bias, void* c,
+                                void* stream) {
+  if (bias == nullptr) return es::fail(ES_ERR_INVALID, "es_contract_bias: null bias");
+  return es::contract(d, a, b, bias, c, stream);
 }

@@ -119,25 +119,35 @@ __device__ __forceinline__ void transpose_block(const uint4 (&in)[4], uint4 (&ou
 }
 
 // ---- incremental K walk ----------------------------------------------------------
-// Fast paths have at most two K sub-axes and the innermost one is a multiple of BK,
-// so the offset of K tile t+1 follows from tile t by additions only.
+// Fast paths have at most kKLevels K sub-axes and the innermost one is a multiple of
+// BK, so the offset of K tile t+1 follows from tile t by one addition: the delta of the
+// lowest level that does not wrap (see ContractArgs::kcnt).
 struct KWalk {
-  uint32_t kin;    // position inside the innermost K sub-axis
-  int64_t off_a;   // element offset of the tile in A
-  int64_t off_b;   // ... in B
+  uint32_t cnt[kKLevels];  // position at each level
+  int64_t off_a;           // element offset of the tile in A
+  int64_t off_b;           // ... in B
   __device__ __forceinline__ void start() {
-    kin = 0;
+#pragma unroll
+    for (int l = 0; l < kKLevels; ++l) cnt[l] = 0;
     off_a = 0;
     off_b = 0;
   }
-  __device__ __forceinline__ void advance(const ContractArgs& p, int bk) {
-    kin += bk;
-    off_a += int64_t(bk) * p.ka_inner;
-    off_b += int64_t(bk) * p.kb_inner;
-    if (kin == p.k_inner) {
-      kin = 0;
-      off_a += p.ka_outer - int64_t(p.k_inner) * p.ka_inner;
-      off_b += p.kb_outer - int64_t(p.k_inner) * p.kb_inner;
+  __device__ __forceinline__ void advance(const ContractArgs& p, int) {
+    int l = 0;
+#pragma unroll
+    for (int e = 0; e + 1 < kKLevels; ++e) {
+      if (l == e && cnt[e] + 1 == p.kcnt[e]) {
+        cnt[e] = 0;
+        l = e + 1;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < kKLevels; ++e) {
+      if (l == e) {
+        cnt[e] += 1;
+        off_a += p.kda[e];
+        off_b += p.kdb[e];
+      }
     }
   }
 };
@@ -395,6 +405,18 @@ __device__ __forceinline__ void store_tile(const ContractArgs& p, void* lds, con
     const uint32_t n = n0 + c;
     col_off[c] = n < p.N ? group_offset_k<2>(&kp->gn, n) : -1;
   }
+  // bias of this lane's columns (es_contract_bias), added before the one rounding; an
+  // accumulator is never -0 (sums start from +0), so adding 0 without bias is exact
+  float bv[FN][4][4];
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t n = n0 + wn * WTN + j * 32 + 8 * g + 4 * (lane / 32) + r;
+        bv[j][g][r] = p.bias != nullptr && n < p.N ? Elem<T>::load(static_cast<const S*>(p.bias)[n]) : 0.f;
+      }
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int srow = wm * 32 + lane % 32;
@@ -406,10 +428,11 @@ __device__ __forceinline__ void store_tile(const ContractArgs& p, void* lds, con
         S* dst = stage + srow * SLD + scol;
         if constexpr (sizeof(S) == 4) {
           *reinterpret_cast<float4*>(dst) =
-              float4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+              float4{acc[i][j][4 * g] + bv[j][g][0], acc[i][j][4 * g + 1] + bv[j][g][1],
+                     acc[i][j][4 * g + 2] + bv[j][g][2], acc[i][j][4 * g + 3] + bv[j][g][3]};
         } else {
-          const float v0 = acc[i][j][4 * g], v1 = acc[i][j][4 * g + 1];
-          const float v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
+          const float v0 = acc[i][j][4 * g] + bv[j][g][0], v1 = acc[i][j][4 * g + 1] + bv[j][g][1];
+          const float v2 = acc[i][j][4 * g + 2] + bv[j][g][2], v3 = acc[i][j][4 * g + 3] + bv[j][g][3];
           *reinterpret_cast<uint2*>(dst) = uint2{Traits<T>::pack2(v0, v1), Traits<T>::pack2(v2, v3)};
         }
       }
@@ -620,29 +643,23 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const Contrac
 // K walk of contract_pipe's copies.  The loop body has no branches: past the last K
 // tile the copies re-fetch the last tile into a stage nobody reads.
 struct PipeWalk {
-  uint32_t t;     // K tile index of the next copy
-  uint32_t kin;   // position inside the innermost K sub-axis
-  int64_t oa, ob; // element offsets of that tile in A and B
-  int64_t da0, db0, da1, db1;  // advance inside the inner sub-axis / across its end
+  uint32_t t;  // K tile index of the next copy
+  KWalk k;     // its offsets in A and B (oa / ob)
+  int64_t oa, ob;
 
-  __device__ __forceinline__ void start(const ContractArgs& p, int bk) {
+  __device__ __forceinline__ void start(const ContractArgs&, int) {
     t = 0;
-    kin = 0;
+    k.start();
     oa = ob = 0;
-    da0 = int64_t(bk) * p.ka_inner;
-    db0 = int64_t(bk) * p.kb_inner;
-    da1 = da0 + p.ka_outer - int64_t(p.k_inner) * p.ka_inner;
-    db1 = db0 + p.kb_outer - int64_t(p.k_inner) * p.kb_inner;
   }
   // next tile, or stay on the last one
   __device__ __forceinline__ void advance(const ContractArgs& p, uint32_t nk, int bk) {
-    const bool step = t + 1 < nk;
-    const uint32_t kin2 = kin + uint32_t(bk);
-    const bool wrap = kin2 == p.k_inner;
-    oa += step ? (wrap ? da1 : da0) : 0;
-    ob += step ? (wrap ? db1 : db0) : 0;
-    kin = step ? (wrap ? 0u : kin2) : kin;
-    t += step ? 1u : 0u;
+    if (t + 1 < nk) {
+      k.advance(p, bk);
+      t += 1;
+      oa = k.off_a;
+      ob = k.off_b;
+    }
   }
 };
 
@@ -800,13 +817,23 @@ __device__ __forceinline__ void store_pipe(const ContractArgs& p, typename Trait
     const uint32_t n = n0 + c;
     col_off[c] = n < p.N ? group_offset_k<2>(&kp->gn, n) : -1;
   }
+  // bias of this lane's columns (es_contract_bias), added before the one rounding; an
+  // accumulator is never -0 (sums start from +0), so adding 0 without bias is exact
+  f32x4 bv[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t n = n0 + wn * WTN + j * 16 + 4 * (lane / 16) + r;
+      bv[j][r] = p.bias != nullptr && n < p.N ? Elem<T>::load(static_cast<const S*>(p.bias)[n]) : 0.f;
+    }
 #pragma unroll
   for (int q = 0; q < P; ++q) {
 #pragma unroll
     for (int ii = 0; ii < BPP; ++ii)
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const f32x4& a = acc[q * BPP + ii][j];
+        const f32x4 a = acc[q * BPP + ii][j] + bv[j];
         *reinterpret_cast<uint2*>(region + (ii * 16 + lane % 16) * SLD + wn * WTN + j * 16 + 4 * (lane / 16)) =
             uint2{Traits<T>::pack2(a[0], a[1]), Traits<T>::pack2(a[2], a[3])};
       }

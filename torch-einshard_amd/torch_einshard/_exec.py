@@ -92,8 +92,11 @@ def _raw_stream(device):
     return torch._C._cuda_getCurrentRawStream(device.index if device.index is not None else torch.cuda.current_device())
 
 
-def launch(prep, xs, device, dtype):
-    """Allocate the output and enqueue ``prep`` on the current stream of ``device``."""
+def launch(prep, xs, device, dtype, bias=None):
+    """Allocate the output and enqueue ``prep`` on the current stream of ``device``.
+
+    ``bias`` (a contraction only): a dense vector over the N group added to every
+    output row before the one rounding (es_contract_bias)."""
     out = torch.empty(prep.out_shape, dtype=dtype, device=device)
     if prep.noop or out.numel() == 0:
         return out
@@ -113,6 +116,13 @@ def launch(prep, xs, device, dtype):
         need = prep.workspace
         ws = torch.empty(need, dtype=torch.uint8, device=device) if need > 0 else None
         status = fn(prep.ref, ptrs[0], ptrs[1], out.data_ptr(), ws.data_ptr() if ws is not None else None, need, stream)
+    elif bias is not None:
+        if prep.entry != "es_contract":
+            raise AssertionError("a bias applies to a contraction only")
+        status = handle.es_contract_bias(prep.ref, *ptrs, bias.data_ptr(), out.data_ptr(), stream)
+        if status < 0:
+            raise _native.NativeError("es_contract_bias", status, handle.es_last_error().decode())
+        return out
     else:
         status = fn(prep.ref, *ptrs, out.data_ptr(), stream)
     if status < 0:

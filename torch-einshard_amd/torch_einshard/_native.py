@@ -136,6 +136,17 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(ContractDesc), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p],
     ),
+    "es_contract_bias": (
+        ctypes.c_int,
+        [
+            ctypes.POINTER(ContractDesc),
+            ctypes.c_void_p,
+            ctypes.c_void_p,
+            ctypes.c_void_p,
+            ctypes.c_void_p,
+            ctypes.c_void_p,
+        ],
+    ),
     "es_abi_version": (ctypes.c_int, []),
     "es_version": (ctypes.c_char_p, []),
     "es_last_error": (ctypes.c_char_p, []),
