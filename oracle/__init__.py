@@ -30,4 +30,8 @@ PINNING = {
         "closed-form brute force (oracle/brute.c)"
     ),
     "einshard_oracle.einhalo_cpu": "pinned: known answers of reference tests/test_halo.py:29-50; brute force",
+    "einshard_oracle.einconv_cpu": (
+        "pinned: the F.conv2d(padding=1) relation of reference tests/test_conv.py:11-78; an fp64 direct sum "
+        "over (kernel, channel) on tiny shapes with dilation, asymmetric halos and every boundary"
+    ),
 }

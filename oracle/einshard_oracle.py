@@ -260,3 +260,42 @@ def einwindow_cpu(expression, x, windows, radius, *, boundary="constant", fill=0
         z = z.unfold(current.index(name), left + right + 1, 1)
         current.append(windows[name])
     return z.permute([current.index(name) for name in out_names]).contiguous()
+
+
+def einconv_cpu(expression, x, weight, windows, *, bias=None, padding=None, dilation=1, boundary="constant", fill=0):
+    """The reference's local einconv (conv.py:153-207) on CPU tensors: pad every
+    window source axis by its halo, permute the input to (batch..., channel,
+    spatial...) and the weight to (out channel, channel, kernel...), run
+    F.conv{1,2,3}d with padding 0, then permute back to the output order.
+    ``padding``: None (the reference default: half the effective kernel per side),
+    an int / (left, right) per axis, or a dict keyed by the source axis."""
+    inputs, out = parse(expression)
+    x_names = _names(inputs[0][0])
+    w_names = _names(inputs[1][0])
+    out_names = _names(out[0])
+    spatial = list(windows)
+    kernels = [windows[name] for name in spatial]
+    ndim = len(spatial)
+    dil = (dilation,) * ndim if isinstance(dilation, int) else tuple(dilation)
+    channel = [n for n in x_names if n in w_names and n not in spatial and n not in out_names][0]
+    out_channel = [n for n in w_names if n in out_names and n not in x_names][0]
+    batch = [n for n in x_names if n not in spatial and n != channel]
+    if padding is None:
+        pads = [(d * (weight.shape[w_names.index(k)] - 1) // 2,) * 2 for k, d in zip(kernels, dil)]
+    elif isinstance(padding, dict):
+        pads = [_normalize(padding[name]) for name in spatial]
+    else:
+        values = (padding,) * ndim if isinstance(padding, int) else tuple(padding)
+        pads = [_normalize(v) for v in values]
+    z = x.cpu()
+    for name, (left, right) in zip(spatial, pads):
+        z = _pad_dim(z, x_names.index(name), left, right, boundary, fill)
+    z = z.permute([x_names.index(n) for n in batch + [channel] + spatial]).contiguous()
+    batch_shape = z.shape[: len(batch)]
+    z = z.reshape((-1, z.shape[len(batch)], *z.shape[len(batch) + 1 :]))
+    w = weight.cpu().permute([w_names.index(n) for n in [out_channel, channel] + kernels]).contiguous()
+    conv = {1: F.conv1d, 2: F.conv2d, 3: F.conv3d}[ndim]
+    r = conv(z, w, None if bias is None else bias.cpu(), stride=1, padding=0, dilation=dil)
+    r = r.reshape((*batch_shape, *r.shape[1:]))
+    conv_names = batch + [out_channel] + spatial
+    return r.permute([conv_names.index(n) for n in out_names]).contiguous()

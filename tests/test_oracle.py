@@ -203,3 +203,105 @@ def test_oracle_parser_rejects_a_tensor_without_axes():
     # reference tests/test_grammar.py:142 and :199 expect "a b ->" to fail
     with pytest.raises(ValueError):
         oracle_parse("a b ->")
+
+
+# ---- einconv: an fp64 direct sum, independent of F.conv ------------------------------
+
+
+def _source_index(i, n, boundary):
+    if 0 <= i < n:
+        return i
+    if boundary == "replicate":
+        return min(max(i, 0), n - 1)
+    if boundary == "periodic":
+        return i % n
+    return None  # constant: the fill value
+
+
+def _conv_direct_f64(x, w, bias, names, windows, pads, dilation, boundary, fill):
+    """out[...] = bias[o] + sum over (kernel..., channel) of w * x at s + d * k - left,
+    by explicit loops over every output element (tiny shapes only)."""
+    import itertools
+
+    x_names, w_names, out_names = names
+    spatial = list(windows)
+    channel = [n for n in x_names if n in w_names and n not in spatial and n not in out_names][0]
+    out_ch = [n for n in w_names if n in out_names and n not in x_names][0]
+    size = {n: x.shape[i] for i, n in enumerate(x_names)}
+    size.update({n: w.shape[i] for i, n in enumerate(w_names)})
+    xd, wd = x.to(torch.float64), w.to(torch.float64)
+    out = torch.zeros([size[n] for n in out_names], dtype=torch.float64)
+    kernels = [windows[s] for s in spatial]
+    for oc in itertools.product(*[range(size[n]) for n in out_names]):
+        at = dict(zip(out_names, oc))
+        total = 0.0 if bias is None else float(bias[at[out_ch]])
+        for kc in itertools.product(*[range(size[k]) for k in kernels], range(size[channel])):
+            k_at = dict(zip(kernels + [channel], kc))
+            xi = []
+            for n in x_names:
+                if n in windows:
+                    j = spatial.index(n)
+                    i = _source_index(at[n] + dilation[j] * k_at[windows[n]] - pads[j][0], size[n], boundary)
+                    if i is None:
+                        break
+                    xi.append(i)
+                else:
+                    xi.append(k_at[n] if n == channel else at[n])
+            xv = float(fill) if len(xi) < len(x_names) else float(xd[tuple(xi)])
+            wi = tuple(at[n] if n == out_ch else k_at[n] for n in w_names)
+            total += float(wd[wi]) * xv
+        out[oc] = total
+    return out
+
+
+CONV_DIRECT_CASES = [
+    # expression, x shape, w shape, windows, padding (per source axis), dilation
+    ("b h c, o c k -> b h o", (2, 7, 3), (4, 3, 3), {"h": "k"}, [(1, 1)], (1,)),
+    ("b h c, o c k -> b o h", (2, 9, 2), (3, 2, 3), {"h": "k"}, [(3, 1)], (2,)),
+    ("b h w c, o c kh kw -> b h w o", (1, 4, 5, 3), (2, 3, 2, 3), {"h": "kh", "w": "kw"}, [(1, 0), (0, 2)], (1, 1)),
+    ("c h b w, kw o kh c -> o w b h", (2, 5, 2, 4), (3, 2, 3, 2), {"h": "kh", "w": "kw"}, [(2, 2), (1, 1)], (2, 1)),
+    ("b d h w c, o c kd kh kw -> b d h w o", (1, 3, 4, 3, 2), (2, 2, 3, 1, 3), {"d": "kd", "h": "kh", "w": "kw"},
+     [(1, 1), (0, 0), (2, 0)], (1, 1, 1)),
+]
+
+
+@pytest.mark.parametrize("boundary", ["constant", "replicate", "periodic"])
+@pytest.mark.parametrize("expr, xs, ws, windows, pads, dilation", CONV_DIRECT_CASES)
+def test_einconv_cpu_matches_direct_sum_f64(expr, xs, ws, windows, pads, dilation, boundary):
+    from oracle.einshard_oracle import einconv_cpu
+
+    x = randn(*xs, seed=41).to(torch.float64)
+    w = randn(*ws, seed=42).to(torch.float64)
+    (x_spec, w_spec), out_spec = oracle_parse(expr)
+    names = [[item[1] for item in spec[0]] for spec in (x_spec, w_spec, out_spec)]
+    out_ch_size = ws[names[1].index([n for n in names[1] if n in names[2] and n not in names[0]][0])]
+    bias = randn(out_ch_size, seed=43).to(torch.float64)
+    padding = {s: p for s, p in zip(windows, pads)}
+    got = einconv_cpu(expr, x, w, windows, bias=bias, padding=padding, dilation=dilation, boundary=boundary, fill=-1.5)
+    want = _conv_direct_f64(x, w, bias, names, windows, pads, dilation, boundary, -1.5)
+    torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_einconv_cpu_is_conv2d_with_padding_one():
+    # reference tests/test_conv.py:11-24: the default padding of a 3 x 3 kernel
+    from oracle.einshard_oracle import einconv_cpu
+
+    x = randn(2, 5, 6, 3, seed=333)
+    w = randn(4, 3, 3, 3, seed=334)
+    bias = randn(4, seed=335)
+    got = einconv_cpu("b h w c, o c kh kw -> b h w o", x, w, {"h": "kh", "w": "kw"}, bias=bias)
+    want = F.conv2d(x.permute(0, 3, 1, 2), w, bias, padding=1).permute(0, 2, 3, 1)
+    torch.testing.assert_close(got, want)
+
+
+def test_planted_flipped_kernel_is_caught():
+    # a true convolution (flipped kernel) instead of the cross-correlation F.conv computes
+    x = randn(1, 6, 2, seed=7).to(torch.float64)
+    w = randn(2, 2, 3, seed=8).to(torch.float64)
+    names = [["b", "h", "c"], ["o", "c", "k"], ["b", "h", "o"]]
+    good = _conv_direct_f64(x, w, None, names, {"h": "k"}, [(1, 1)], (1,), "constant", 0)
+    flipped = _conv_direct_f64(x, w.flip(-1), None, names, {"h": "k"}, [(1, 1)], (1,), "constant", 0)
+    assert not torch.allclose(good, flipped)
+    from oracle.einshard_oracle import einconv_cpu
+
+    torch.testing.assert_close(einconv_cpu("b h c, o c k -> b h o", x, w, {"h": "k"}), good)

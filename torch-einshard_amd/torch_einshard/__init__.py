@@ -2,7 +2,8 @@
 
 Public surface kept from the reference (src/torch_einshard/__init__.py:1-57,
 346-372): ``einshard``, ``einshard_like``, ``einwindow``, ``einhalo``, the
-notation types, ``PlanPolicy`` / ``optimize`` and the plan diagnostics.
+notation types, ``PlanPolicy`` / ``optimize`` and the plan diagnostics, and
+``einconv`` (src/torch_einshard/conv.py:65).
 Arithmetic runs on hand-written HIP kernels (libeinshard_hip.so) on ROCm
 device tensors; there is no CPU path and no fallback to ``torch.einsum``.
 """
@@ -11,6 +12,7 @@ from . import symbolic
 from ._cache import call_key, lookup, remember
 from ._exec import launch
 from .autograd import needs_grad
+from .conv import einconv
 from .distributed import distributed_1d
 from .einsum import einsum, equation_of, prepare_local
 from .families import cached_expand_axis_families
@@ -36,6 +38,7 @@ __all__ = [
     "einshard_like",
     "einwindow",
     "einhalo",
+    "einconv",
     "einsum",
     "equation_of",
     "parse_sharding",
