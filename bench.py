@@ -1,14 +1,15 @@
 """Benchmark of torch_einshard's MI355X path (one JSON line per workload).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c1|c2|c3|c5a|c5b|c5c|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c1|c2|c3|c5a|c5b|c5c|conv|all]
 
-A step is one es.einshard / es.einwindow call over one batch of synthetic
+A step is one es.einshard / es.einwindow / es.einconv call over one batch of synthetic
 input that is already resident in HBM.  The default workload is config 4 of
 BASELINE.json — one rank's share of a tensor-parallel contraction,
 es.einshard("b n c, h c -> b n h") with x[8,2048,4096], w[1792,4096] bf16 —
 the configuration the north star's headline target (>= 70 % of bf16 MFMA peak)
 is quoted on.  The other configs are parity cases; ``--workload`` measures them
-individually with the same method.
+individually with the same method.  ``conv`` (not a BASELINE config) measures
+es.einconv, the halo + convolution the reference runs through F.conv2d.
 
 Timing: W untimed warm-up steps, then K back-to-back steps between two device
 synchronisations (wall clock -> ms_per_step, value: host work included).  The
@@ -19,7 +20,8 @@ they run back to back without host gaps.  For HBM-bound workloads K more
 launches follow, each after a 512 MiB read that evicts the 256 MB Infinity
 Cache (not timed): roofline.kernel_ms_cold.
 
-roofline.achieved uses algorithmic work only: 2*M*N*K flops for contractions,
+roofline.achieved uses algorithmic work only: 2*M*N*K flops for contractions
+(for einconv, of the implicit GEMM alone, timed without the two gathers around it),
 unique input bytes + output bytes for the copy / reduce / broadcast kernels.
 cpu_baseline times the reference's CPU path as restated by oracle/ on the host
 cores (torch.einsum / F.pad + unfold + permute on CPU tensors) on a bounded
@@ -181,6 +183,27 @@ def wl_c5c(dev):
     )
 
 
+def wl_conv(dev):
+    g = _gen()
+    x = torch.randn(16, 64, 64, 256, generator=g).to(torch.bfloat16)
+    w = (torch.randn(256, 256, 3, 3, generator=g) * 0.02).to(torch.bfloat16)
+    b = torch.randn(256, generator=g).to(torch.bfloat16)
+    return dict(
+        key="conv",
+        workload=(
+            "einconv: es.einconv('b h w c, o c kh kw -> b h w o', {h:kh, w:kw}, bias) x[16,64,64,256] "
+            "w[256,256,3,3] bf16, same padding, forward (checkpoint=False)"
+        ),
+        conv=("b h w c, o c kh kw -> b h w o", {"h": "kh", "w": "kw"}),
+        host=[x, w, b],
+        flops=2 * (16 * 64 * 64) * 256 * (9 * 256),
+        dtype="bf16",
+        bound="mfma",
+        peak=PEAK["bf16"],
+        sample=lambda xs: ([xs[0][:1], xs[1], xs[2]], 1 / 16),
+    )
+
+
 def wl_copy(dev):
     """Calibration: a plain 1 GiB copy through the same gather kernel (known traffic)."""
     x = torch.empty(16384, 16384, dtype=torch.float32).fill_(1.0)
@@ -205,11 +228,15 @@ WORKLOADS = {
     "c5a": wl_c5a,
     "c5b": wl_c5b,
     "c5c": wl_c5c,
+    "conv": wl_conv,
     "copy": wl_copy,
 }
 
 
 def _runner(es, wl):
+    if "conv" in wl:
+        expr, windows = wl["conv"]
+        return lambda xs: es.einconv(expr, xs[0], xs[1], windows, bias=xs[2], checkpoint=False)
     if "window" in wl:
         expr, windows, radius = wl["window"]
         return lambda xs: es.einwindow(expr, xs[0], windows, radius)
@@ -217,9 +244,24 @@ def _runner(es, wl):
     return lambda xs: es.einshard(expr, *xs)
 
 
-def _cpu_runner(wl):
-    from oracle.einshard_oracle import einshard_cpu, einwindow_cpu
+def _kernel_runner(es, wl, xs):
+    """The dominant kernel alone: for einconv the implicit GEMM on operands already
+    gathered (padded input, weight in (out channel, kernel..., channel) order)."""
+    if "conv" not in wl:
+        return _runner(es, wl), xs
+    from torch_einshard.conv import _conv
 
+    xp = es.einhalo("b h w c", xs[0], {"h": 1, "w": 1})
+    wk = es.einshard("o c kh kw -> o kh kw c", xs[1])
+    return (lambda ys: _conv(ys[0], ys[1], ys[2], (1, 1), (0, 1, 2, 3))), [xp, wk, xs[2]]
+
+
+def _cpu_runner(wl):
+    from oracle.einshard_oracle import einconv_cpu, einshard_cpu, einwindow_cpu
+
+    if "conv" in wl:
+        expr, windows = wl["conv"]
+        return lambda xs: einconv_cpu(expr, xs[0], xs[1], windows, bias=xs[2])
     if "window" in wl:
         expr, windows, radius = wl["window"]
         return lambda xs: einwindow_cpu(expr, xs[0], windows, radius)
@@ -244,6 +286,9 @@ def measure_gpu(es, wl, dev, steps, warmup):
     # kernel time: the same K launches behind a bounded spin kernel, so that the
     # host has enqueued all of them before the first starts and the two events
     # bracket back-to-back kernels only (no host gaps)
+    run, xs = _kernel_runner(es, wl, xs)
+    out = run(xs)
+    torch.cuda.synchronize(dev)
     torch.cuda._sleep(PRIME_CYCLES)
     start.record(stream)
     for _ in range(steps):
