@@ -34,4 +34,8 @@ PINNING = {
         "pinned: the F.conv2d(padding=1) relation of reference tests/test_conv.py:11-78; an fp64 direct sum "
         "over (kernel, channel) on tiny shapes with dilation, asymmetric halos and every boundary"
     ),
+    "einshard_oracle.einroll_cpu": (
+        "pinned: the explicit index map out[i] = x[(i - s) mod n] on tiny shapes (negative, large and "
+        "multiple-of-n shifts); the torch.roll expectation of reference tests/test_distributed_roll.py:10-20"
+    ),
 }

@@ -13,6 +13,11 @@ the reference's result on the same inputs:
                   wrapped ``index_select``) via :307-344.
   einwindow_cpu   reference halo.py:347-418: the halo above, then ``unfold`` per
                   windowed axis in input order, then ``permute(...).contiguous()``.
+  einconv_cpu     reference conv.py:153-207: the halo, permutes to (batch,
+                  channel, spatial...) and (out, channel, kernel...), then
+                  ``F.conv{1,2,3}d`` with padding 0.
+  einroll_cpu     reference roll.py:10-45 (local axes): ``torch.roll`` per axis
+                  with a nonzero shift, in spec order; ``x`` itself if none.
 
 The expression parser here is deliberately independent of the product's: a
 small tokenizer that accepts the expressions the tests use (axes, ``name/mesh``,
@@ -299,3 +304,15 @@ def einconv_cpu(expression, x, weight, windows, *, bias=None, padding=None, dila
     r = r.reshape((*batch_shape, *r.shape[1:]))
     conv_names = batch + [out_channel] + spatial
     return r.permute([conv_names.index(n) for n in out_names]).contiguous()
+
+
+def einroll_cpu(spec, x, shifts):
+    """The reference's local einroll (roll.py:10-27): one ``torch.roll`` per axis of
+    the spec with a nonzero shift, dims numbered by spec position."""
+    inputs, _ = parse(f"{spec} -> {spec}")
+    z = x
+    for dim, name in enumerate(_names(inputs[0][0])):
+        shift = shifts.get(name, 0)
+        if shift != 0:
+            z = torch.roll(z.cpu(), shifts=shift, dims=dim)
+    return z

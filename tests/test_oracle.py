@@ -305,3 +305,56 @@ def test_planted_flipped_kernel_is_caught():
     from oracle.einshard_oracle import einconv_cpu
 
     torch.testing.assert_close(einconv_cpu("b h c, o c k -> b h o", x, w, {"h": "k"}), good)
+
+
+# ---- einroll: the modular index map ------------------------------------------------------
+
+
+def _roll_index_map(x, shifts_by_dim):
+    """out[i...] = x[(i_d - s_d) mod n_d ...] by explicit index arithmetic."""
+    out = torch.empty_like(x)
+    flat = x.reshape(-1)
+    strides = [1] * x.dim()
+    for d in range(x.dim() - 2, -1, -1):
+        strides[d] = strides[d + 1] * x.shape[d + 1]
+    for linear in range(x.numel()):
+        rem, src = linear, 0
+        for d in range(x.dim()):
+            i = rem // strides[d]
+            rem -= i * strides[d]
+            src += ((i - shifts_by_dim.get(d, 0)) % x.shape[d]) * strides[d]
+        out.view(-1)[linear] = flat[src]
+    return out
+
+
+@pytest.mark.parametrize(
+    "spec, shape, shifts, by_dim",
+    [
+        ("a b", (5, 4), {"a": 2}, {0: 2}),
+        ("a b", (5, 4), {"a": -7, "b": 3}, {0: -7, 1: 3}),
+        ("b h w c", (2, 4, 6, 3), {"h": 3, "w": -5}, {1: 3, 2: -5}),
+        ("t x", (3, 5), {"x": 10, "t": 1}, {0: 1, 1: 10}),
+        ("t x", (3, 5), {"z": 2}, {}),
+    ],
+)
+def test_einroll_cpu_matches_index_map(spec, shape, shifts, by_dim):
+    from oracle.einshard_oracle import einroll_cpu
+
+    x = torch.arange(int(torch.tensor(shape).prod())).reshape(shape)
+    assert torch.equal(einroll_cpu(spec, x, shifts), _roll_index_map(x, by_dim))
+
+
+def test_einroll_cpu_reference_family_case():
+    # reference tests/test_distributed_roll.py:10-20, families already expanded
+    from oracle.einshard_oracle import einroll_cpu
+
+    x = randn(2, 3, 4, 5, 6, 7, seed=5)
+    got = einroll_cpu("b t h w d c", x, {"h": 1, "w": -2, "d": 3})
+    assert torch.equal(got, _roll_index_map(x, {2: 1, 3: -2, 4: 3}))
+
+
+def test_planted_roll_direction_is_caught():
+    from oracle.einshard_oracle import einroll_cpu
+
+    x = torch.arange(12).reshape(3, 4)
+    assert not torch.equal(einroll_cpu("a b", x, {"b": 1}), _roll_index_map(x, {1: -1}))

@@ -3,7 +3,8 @@
 Public surface kept from the reference (src/torch_einshard/__init__.py:1-57,
 346-372): ``einshard``, ``einshard_like``, ``einwindow``, ``einhalo``, the
 notation types, ``PlanPolicy`` / ``optimize`` and the plan diagnostics, and
-``einconv`` (src/torch_einshard/conv.py:65).
+``einconv`` (src/torch_einshard/conv.py:65) and ``einroll``
+(src/torch_einshard/roll.py:10).
 Arithmetic runs on hand-written HIP kernels (libeinshard_hip.so) on ROCm
 device tensors; there is no CPU path and no fallback to ``torch.einsum``.
 """
@@ -18,6 +19,7 @@ from .einsum import einsum, equation_of, prepare_local
 from .families import cached_expand_axis_families
 from .grammar import Axes, parse_sharding
 from .halo import einhalo, einwindow
+from .roll import einroll
 from .sharding import Axis, AxisGroup, EllipsisAxis, TensorAnnotation, TensorSpec
 from .symbolic import (
     ExecutionPlan,
@@ -39,6 +41,7 @@ __all__ = [
     "einwindow",
     "einhalo",
     "einconv",
+    "einroll",
     "einsum",
     "equation_of",
     "parse_sharding",
