@@ -1,6 +1,7 @@
 """Benchmark of torch_einshard's MI355X path (one JSON line per workload).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c4|c1|c2|c3|c5a|c5b|c5c|conv|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload c4|c1|c2|c3|c5a|c5b|c5c|conv|partition|roll|all]
 
 A step is one es.einshard / es.einwindow / es.einconv call over one batch of synthetic
 input that is already resident in HBM.  The default workload is config 4 of
@@ -9,7 +10,9 @@ es.einshard("b n c, h c -> b n h") with x[8,2048,4096], w[1792,4096] bf16 —
 the configuration the north star's headline target (>= 70 % of bf16 MFMA peak)
 is quoted on.  The other configs are parity cases; ``--workload`` measures them
 individually with the same method.  ``conv`` (not a BASELINE config) measures
-es.einconv, the halo + convolution the reference runs through F.conv2d.
+es.einconv, the halo + convolution the reference runs through F.conv2d;
+``partition`` and ``roll`` are the reference's own local benchmarks of a family
+permute and of einroll (benchmarks/bench_local.py, "large" size).
 
 Timing: W untimed warm-up steps, then K back-to-back steps between two device
 synchronisations (wall clock -> ms_per_step, value: host work included).  The
@@ -18,7 +21,10 @@ the stream the kernel runs on (torch's current stream, which the library
 launches on) around K more launches queued behind a bounded spin kernel, so
 they run back to back without host gaps.  For HBM-bound workloads K more
 launches follow, each after a 512 MiB read that evicts the 256 MB Infinity
-Cache (not timed): roofline.kernel_ms_cold.
+Cache (not timed): roofline.kernel_ms_cold.  As in ``timeit``, Python's cyclic
+garbage collector is run before and switched off during the timed loops: a
+full collection pauses the interpreter for tens of milliseconds at a random
+call and has nothing to do with the library.
 
 roofline.achieved uses algorithmic work only: 2*M*N*K flops for contractions
 (for einconv, of the implicit GEMM alone, timed without the two gathers around it),
@@ -29,6 +35,7 @@ sample of the same workload, scaled to the same unit.
 """
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -204,6 +211,58 @@ def wl_conv(dev):
     )
 
 
+def wl_partition(dev):
+    g = _gen()
+    x = torch.randn(4, 2, 128, 128, 128, generator=g)
+    families = {"spatial": ("h", "w"), "window": ("wh", "ww")}
+    return dict(
+        key="partition",
+        workload=(
+            "window partition (reference benchmarks/bench_local.py:95-126, large): es.einshard('b t "
+            "[*spatial *window] c -> (b *spatial) t *window c', families, sizes={window: (8, 8)}) "
+            "x[4,2,128,128,128] fp32"
+        ),
+        gpu_call=lambda es, xs: es.einshard(
+            "b t [*spatial *window] c -> (b *spatial) t *window c", xs[0], families=families, sizes={"window": (8, 8)}
+        ),
+        cpu_call=lambda xs: _oracle().einshard_cpu(
+            "b t (h wh) (w ww) c -> (b h w) t wh ww c", xs[0], sizes={"wh": 8, "ww": 8}
+        ),
+        host=[x],
+        bytes=2 * 4 * 2 * 128 * 128 * 128 * 4,
+        dtype="f32",
+        bound="hbm",
+        peak=PEAK["hbm"],
+        sample=lambda xs: ([xs[0][:1]], 1 / 4),
+    )
+
+
+def wl_roll(dev):
+    g = _gen()
+    x = torch.randn(4, 128, 128, 128, generator=g)
+    return dict(
+        key="roll",
+        workload=(
+            "einroll (reference benchmarks/bench_local.py:212-229, large): es.einroll('b h w c', "
+            "{h: 3, w: -5}) x[4,128,128,128] fp32"
+        ),
+        gpu_call=lambda es, xs: es.einroll("b h w c", xs[0], {"h": 3, "w": -5}),
+        cpu_call=lambda xs: _oracle().einroll_cpu("b h w c", xs[0], {"h": 3, "w": -5}),
+        host=[x],
+        bytes=2 * 4 * 128 * 128 * 128 * 4,
+        dtype="f32",
+        bound="hbm",
+        peak=PEAK["hbm"],
+        sample=lambda xs: ([xs[0][:1]], 1 / 4),
+    )
+
+
+def _oracle():
+    from oracle import einshard_oracle
+
+    return einshard_oracle
+
+
 def wl_copy(dev):
     """Calibration: a plain 1 GiB copy through the same gather kernel (known traffic)."""
     x = torch.empty(16384, 16384, dtype=torch.float32).fill_(1.0)
@@ -229,11 +288,15 @@ WORKLOADS = {
     "c5b": wl_c5b,
     "c5c": wl_c5c,
     "conv": wl_conv,
+    "partition": wl_partition,
+    "roll": wl_roll,
     "copy": wl_copy,
 }
 
 
 def _runner(es, wl):
+    if "gpu_call" in wl:
+        return lambda xs: wl["gpu_call"](es, xs)
     if "conv" in wl:
         expr, windows = wl["conv"]
         return lambda xs: es.einconv(expr, xs[0], xs[1], windows, bias=xs[2], checkpoint=False)
@@ -259,6 +322,8 @@ def _kernel_runner(es, wl, xs):
 def _cpu_runner(wl):
     from oracle.einshard_oracle import einconv_cpu, einshard_cpu, einwindow_cpu
 
+    if "cpu_call" in wl:
+        return wl["cpu_call"]
     if "conv" in wl:
         expr, windows = wl["conv"]
         return lambda xs: einconv_cpu(expr, xs[0], xs[1], windows, bias=xs[2])
@@ -270,6 +335,15 @@ def _cpu_runner(wl):
 
 
 def measure_gpu(es, wl, dev, steps, warmup):
+    gc.collect()
+    gc.disable()
+    try:
+        return _measure_gpu(es, wl, dev, steps, warmup)
+    finally:
+        gc.enable()
+
+
+def _measure_gpu(es, wl, dev, steps, warmup):
     xs = [t.to(dev) for t in wl["host"]]
     run = _runner(es, wl)
     for _ in range(warmup):
@@ -303,7 +377,8 @@ def measure_gpu(es, wl, dev, steps, warmup):
         # one (a 512 MiB read, not timed; a read leaves no dirty lines behind to
         # be written back during the timed launch): shows whether back-to-back
         # steps were served from cache
-        flush = torch.ones(512 * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
+        # (float32: a sum of int32 would first convert to int64, writing 1 GiB)
+        flush = torch.ones(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
         events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
         for s, e in events:
             flush.sum()
