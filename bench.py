@@ -444,6 +444,7 @@ def bench_one(es, key, dev, steps, warmup, cpu=True):
         unit=unit,
         frac=round(achieved / wl["peak"], 4),
         traffic=_traffic(key),
+        **_mfma(key),
         kernel=g["kernel"],
         kernel_ms=round(g["kernel_ms"], 5),
     )
@@ -467,6 +468,37 @@ def bench_one(es, key, dev, steps, warmup, cpu=True):
         "cpu_baseline": measure_cpu(wl) if cpu else None,
     }
     return line
+
+
+def _profile_rows(name, key_cells):
+    """Rows of a markdown table in profiles/<name> keyed by their first cell."""
+    path = os.path.join(_REPO, "profiles", name)
+    if not os.path.exists(path):
+        return None, {}
+    header, rows = None, {}
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if header is None and all(k in cells for k in key_cells):
+            header = cells
+        elif header is not None and len(cells) == len(header) and not cells[0].startswith("---"):
+            rows[cells[0]] = cells
+    return header, rows
+
+
+def _mfma(key):
+    """Clock (GHz) and MFMA utilisation of a contraction workload's kernel, measured with
+    the rocprofv3 counters GRBM_GUI_ACTIVE and SQ_VALU_MFMA_BUSY_CYCLES (profiles/mfma.md)."""
+    header, rows = _profile_rows("mfma.md", ("clock GHz", "MFMA util"))
+    if key not in rows:
+        return {}
+    cells = rows[key]
+    try:
+        return {
+            "clock_ghz": float(cells[header.index("clock GHz")]),
+            "mfma_util": round(float(cells[header.index("MFMA util")].rstrip(" %")) / 100, 4),
+        }
+    except ValueError:
+        return {}
 
 
 def _traffic(key):
