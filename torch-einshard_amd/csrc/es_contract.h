@@ -75,6 +75,7 @@ struct ContractArgs {
   // the L-th sub-axis out.  Advancing at level L (every level below it wrapping) adds
   // kda[L] / kdb[L] to the tile's offset in A / B.
   uint32_t kcnt[kKLevels];  // extent of each level (unused levels: never wrap)
+  uint32_t klevels;         // levels in use: 1, 2, or kKLevels (3 or 4 K sub-axes)
   int64_t kda[kKLevels];
   int64_t kdb[kKLevels];
   const void* bias;      // es_contract_bias: bias[n] added before rounding; else null

@@ -106,6 +106,7 @@ void k_walk(const es_contract_desc* d, int bk, ContractArgs& p) {
     p.kcnt[l] = 0xffffffffu;
     p.kda[l] = p.kdb[l] = 0;
   }
+  p.klevels = d->n_k <= 1 ? 1 : (d->n_k == 2 ? 2 : kKLevels);
   if (d->n_k == 0 || d->n_k > kKLevels) return;
   const es_axis& in = d->k[d->n_k - 1];
   const int64_t tiles = in.size / bk;

@@ -121,34 +121,63 @@ __device__ __forceinline__ void transpose_block(const uint4 (&in)[4], uint4 (&ou
 // ---- incremental K walk ----------------------------------------------------------
 // Fast paths have at most kKLevels K sub-axes and the innermost one is a multiple of
 // BK, so the offset of K tile t+1 follows from tile t by one addition: the delta of the
-// lowest level that does not wrap (see ContractArgs::kcnt).
+// lowest level that does not wrap (see ContractArgs::kcnt).  L is the number of levels
+// the walk keeps (1, 2 or kKLevels; levels beyond the descriptor's never wrap).  The
+// limits and deltas are read from the kernel arguments once, at start, and kept in
+// (scalar) registers: an advance is a handful of compares and selects, with no memory
+// access that could make the wave wait behind its LDS reads.
+template <int L>
 struct KWalk {
-  uint32_t cnt[kKLevels];  // position at each level
-  int64_t off_a;           // element offset of the tile in A
-  int64_t off_b;           // ... in B
-  __device__ __forceinline__ void start() {
+  static constexpr int W = L > 1 ? L - 1 : 1;  // levels that can wrap (all but the outermost)
+  uint32_t cnt[W];  // position at each wrapping level
+  uint32_t lim[W];  // its extent
+  int64_t da[L], db[L];
+  int64_t off_a;  // element offset of the tile in A
+  int64_t off_b;  // ... in B
+  __device__ __forceinline__ void start(const ContractArgs& p) {
 #pragma unroll
-    for (int l = 0; l < kKLevels; ++l) cnt[l] = 0;
+    for (int l = 0; l < W; ++l) {
+      cnt[l] = 0;
+      lim[l] = p.kcnt[l];
+    }
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+      da[l] = p.kda[l];
+      db[l] = p.kdb[l];
+    }
     off_a = 0;
     off_b = 0;
   }
-  __device__ __forceinline__ void advance(const ContractArgs& p, int) {
-    int l = 0;
+  // the step from K tile t to t + 1
+  __device__ __forceinline__ void next(int64_t& sa, int64_t& sb, uint32_t (&c)[W]) const {
+    sa = da[L - 1];
+    sb = db[L - 1];
 #pragma unroll
-    for (int e = 0; e + 1 < kKLevels; ++e) {
-      if (l == e && cnt[e] + 1 == p.kcnt[e]) {
-        cnt[e] = 0;
-        l = e + 1;
+    for (int l = 0; l < W; ++l) c[l] = cnt[l];
+    if constexpr (L > 1) {
+      // the lowest level that does not wrap takes the increment (and its delta); the
+      // levels below it wrap to 0; if every wrapping level wraps, the outermost level
+      // takes it and sa / sb keep its delta
+      bool done = false;
+#pragma unroll
+      for (int l = 0; l < L - 1; ++l) {
+        const bool wrap = cnt[l] + 1 == lim[l];
+        const bool inc = !done && !wrap;
+        sa = inc ? da[l] : sa;
+        sb = inc ? db[l] : sb;
+        c[l] = done ? cnt[l] : (wrap ? 0u : cnt[l] + 1);
+        done = done || !wrap;
       }
     }
+  }
+  __device__ __forceinline__ void advance() {
+    int64_t sa, sb;
+    uint32_t c[W];
+    next(sa, sb, c);
+    off_a += sa;
+    off_b += sb;
 #pragma unroll
-    for (int e = 0; e < kKLevels; ++e) {
-      if (l == e) {
-        cnt[e] += 1;
-        off_a += p.kda[e];
-        off_b += p.kdb[e];
-      }
-    }
+    for (int l = 0; l < W; ++l) cnt[l] = c[l];
   }
 };
 
@@ -377,7 +406,7 @@ constexpr int epilogue_bytes() {
 // along n when n is the output's contiguous axis, element stores otherwise.  `lds`
 // holds at least epilogue_bytes(); the caller has drained every copy into LDS and
 // synchronised the work-group.
-template <typename T, int BM, int BN, int WM, int WN, int FM, int FN>
+template <typename T, int BM, int BN, int WM, int WN, int FM, int FN, bool BIAS>
 __device__ __forceinline__ void store_tile(const ContractArgs& p, void* lds, const f32x16 (&acc)[FM][FN], uint32_t m0,
                                            uint32_t n0, int64_t boff_c) {
   using S = typename Traits<T>::S;
@@ -405,8 +434,7 @@ __device__ __forceinline__ void store_tile(const ContractArgs& p, void* lds, con
     const uint32_t n = n0 + c;
     col_off[c] = n < p.N ? group_offset_k<2>(&kp->gn, n) : -1;
   }
-  // bias of this lane's columns (es_contract_bias), added before the one rounding; an
-  // accumulator is never -0 (sums start from +0), so adding 0 without bias is exact
+  // BIAS: the bias of this lane's columns (es_contract_bias), added before the one rounding
   float bv[FN][4][4];
 #pragma unroll
   for (int j = 0; j < FN; ++j)
@@ -415,8 +443,10 @@ __device__ __forceinline__ void store_tile(const ContractArgs& p, void* lds, con
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const uint32_t n = n0 + wn * WTN + j * 32 + 8 * g + 4 * (lane / 32) + r;
-        bv[j][g][r] = p.bias != nullptr && n < p.N ? Elem<T>::load(static_cast<const S*>(p.bias)[n]) : 0.f;
+        bv[j][g][r] = BIAS && n < p.N ? Elem<T>::load(static_cast<const S*>(p.bias)[n]) : 0.f;
       }
+  // without a bias nothing is added (bv is then unused and folds away)
+  auto biased = [&](float v, int j, int g, int r) { return BIAS ? v + bv[j][g][r] : v; };
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int srow = wm * 32 + lane % 32;
@@ -428,11 +458,11 @@ __device__ __forceinline__ void store_tile(const ContractArgs& p, void* lds, con
         S* dst = stage + srow * SLD + scol;
         if constexpr (sizeof(S) == 4) {
           *reinterpret_cast<float4*>(dst) =
-              float4{acc[i][j][4 * g] + bv[j][g][0], acc[i][j][4 * g + 1] + bv[j][g][1],
-                     acc[i][j][4 * g + 2] + bv[j][g][2], acc[i][j][4 * g + 3] + bv[j][g][3]};
+              float4{biased(acc[i][j][4 * g], j, g, 0), biased(acc[i][j][4 * g + 1], j, g, 1),
+                     biased(acc[i][j][4 * g + 2], j, g, 2), biased(acc[i][j][4 * g + 3], j, g, 3)};
         } else {
-          const float v0 = acc[i][j][4 * g] + bv[j][g][0], v1 = acc[i][j][4 * g + 1] + bv[j][g][1];
-          const float v2 = acc[i][j][4 * g + 2] + bv[j][g][2], v3 = acc[i][j][4 * g + 3] + bv[j][g][3];
+          const float v0 = biased(acc[i][j][4 * g], j, g, 0), v1 = biased(acc[i][j][4 * g + 1], j, g, 1);
+          const float v2 = biased(acc[i][j][4 * g + 2], j, g, 2), v3 = biased(acc[i][j][4 * g + 3], j, g, 3);
           *reinterpret_cast<uint2*>(dst) = uint2{Traits<T>::pack2(v0, v1), Traits<T>::pack2(v2, v3)};
         }
       }
@@ -548,10 +578,10 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const Contrac
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const uint32_t nk = (p.K + BK - 1) / BK;
-  KWalk kw;  // offset of the next tile to fetch
-  kw.start();
-  KWalk tw;  // offset of the next tile to touch
-  tw.start();
+  KWalk<kKLevels> kw;  // offset of the next tile to fetch
+  kw.start(p);
+  KWalk<kKLevels> tw;  // offset of the next tile to touch
+  tw.start(p);
   if (nk > 0) {
     la.issue(&lds[0], kw.off_a);
     lb.issue(&lds[BM * BK], kw.off_b);
@@ -559,13 +589,13 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const Contrac
     lb.load(p, 0, kw.off_b);
     la.store(&lds[0]);
     lb.store(&lds[BM * BK]);
-    if (!kGen) kw.advance(p, BK);
+    if (!kGen) kw.advance();
     if constexpr (kTouch) {
-      tw.advance(p, BK);
+      tw.advance();
 #pragma unroll
       for (int d = 1; d < PF; ++d) {
         if (uint32_t(d) < nk) touch(tw.off_a, tw.off_b);
-        if (uint32_t(d) < nk) tw.advance(p, BK);
+        if (uint32_t(d) < nk) tw.advance();
       }
     }
   }
@@ -596,11 +626,11 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const Contrac
       lb.issue(nxt + BM * BK, kw.off_b);
       la.load(p, (kt + 1) * BK, kw.off_a);
       lb.load(p, (kt + 1) * BK, kw.off_b);
-      if (!kGen) kw.advance(p, BK);
+      if (!kGen) kw.advance();
       if constexpr (kTouch) {
         if (kt + PF < nk) {
           touch(tw.off_a, tw.off_b);
-          tw.advance(p, BK);
+          tw.advance();
         }
       }
     }
@@ -636,30 +666,35 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void contract_kernel(const Contrac
   __syncthreads();
 
   static_assert(epilogue_bytes<S, BM, BN, WM>() <= int(sizeof(lds)), "epilogue must fit in LDS");
-  store_tile<T, BM, BN, WM, WN>(p, lds, acc, m0, n0, boff_c);
+  if (p.bias != nullptr) store_tile<T, BM, BN, WM, WN, FM, FN, true>(p, lds, acc, m0, n0, boff_c);
+  else store_tile<T, BM, BN, WM, WN, FM, FN, false>(p, lds, acc, m0, n0, boff_c);
 }
 
 // ---- software-pipelined kernel, both operands K-contiguous (pieces) ----------------
 // K walk of contract_pipe's copies.  The loop body has no branches: past the last K
 // tile the copies re-fetch the last tile into a stage nobody reads.
+template <int L>
 struct PipeWalk {
   uint32_t t;  // K tile index of the next copy
-  KWalk k;     // its offsets in A and B (oa / ob)
+  KWalk<L> k;  // its offsets in A and B (oa / ob)
   int64_t oa, ob;
 
-  __device__ __forceinline__ void start(const ContractArgs&, int) {
+  __device__ __forceinline__ void start(const ContractArgs& p) {
     t = 0;
-    k.start();
+    k.start(p);
     oa = ob = 0;
   }
-  // next tile, or stay on the last one
-  __device__ __forceinline__ void advance(const ContractArgs& p, uint32_t nk, int bk) {
-    if (t + 1 < nk) {
-      k.advance(p, bk);
-      t += 1;
-      oa = k.off_a;
-      ob = k.off_b;
-    }
+  // next tile, or stay on the last one (branch-free)
+  __device__ __forceinline__ void advance(uint32_t nk) {
+    const bool step = t + 1 < nk;
+    int64_t sa, sb;
+    uint32_t c[KWalk<L>::W];
+    k.next(sa, sb, c);
+    oa += step ? sa : 0;
+    ob += step ? sb : 0;
+#pragma unroll
+    for (int l = 0; l < KWalk<L>::W; ++l) k.cnt[l] = step ? c[l] : k.cnt[l];
+    t += step ? 1u : 0u;
   }
 };
 
@@ -786,7 +821,7 @@ __device__ __forceinline__ void pipe_drain(f32x4 (&acc)[FM][FN]) {
 // the whole work-group writes the rows out (16-byte streaming stores along n when n is
 // the output's contiguous axis, element stores otherwise).  The caller has drained
 // every copy into LDS and synchronised the work-group.
-template <typename T, int BN, int FM, int FN>
+template <typename T, int BN, int FM, int FN, bool BIAS>
 __device__ __forceinline__ void store_pipe(const ContractArgs& p, typename Traits<T>::S* lds0,
                                            typename Traits<T>::S* lds1, const f32x4 (&acc)[FM][FN], uint32_t m0,
                                            uint32_t n0, int64_t boff_c) {
@@ -817,15 +852,14 @@ __device__ __forceinline__ void store_pipe(const ContractArgs& p, typename Trait
     const uint32_t n = n0 + c;
     col_off[c] = n < p.N ? group_offset_k<2>(&kp->gn, n) : -1;
   }
-  // bias of this lane's columns (es_contract_bias), added before the one rounding; an
-  // accumulator is never -0 (sums start from +0), so adding 0 without bias is exact
+  // BIAS: the bias of this lane's columns (es_contract_bias), added before the one rounding
   f32x4 bv[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t n = n0 + wn * WTN + j * 16 + 4 * (lane / 16) + r;
-      bv[j][r] = p.bias != nullptr && n < p.N ? Elem<T>::load(static_cast<const S*>(p.bias)[n]) : 0.f;
+      bv[j][r] = BIAS && n < p.N ? Elem<T>::load(static_cast<const S*>(p.bias)[n]) : 0.f;
     }
 #pragma unroll
   for (int q = 0; q < P; ++q) {
@@ -833,7 +867,7 @@ __device__ __forceinline__ void store_pipe(const ContractArgs& p, typename Trait
     for (int ii = 0; ii < BPP; ++ii)
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const f32x4 a = acc[q * BPP + ii][j] + bv[j];
+        const f32x4 a = BIAS ? acc[q * BPP + ii][j] + bv[j] : acc[q * BPP + ii][j];
         *reinterpret_cast<uint2*>(region + (ii * 16 + lane % 16) * SLD + wn * WTN + j * 16 + 4 * (lane / 16)) =
             uint2{Traits<T>::pack2(a[0], a[1]), Traits<T>::pack2(a[2], a[3])};
       }
@@ -868,7 +902,7 @@ __device__ __forceinline__ void store_pipe(const ContractArgs& p, typename Trait
   }
 }
 
-template <typename T, int BN>
+template <typename T, int BN, int L>
 __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   using S = typename Traits<T>::S;
   constexpr int BM = 256, WM = 2, WN = 2;
@@ -929,8 +963,8 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   };
 
   const uint32_t nk = (p.K + BK - 1) / BK;  // >= 1: an empty K takes the generic kernel
-  PipeWalk w;
-  w.start(p, BK);
+  PipeWalk<L> w;
+  w.start(p);
   const uint32_t lds0_addr = lds_address(lds0);
   const uint32_t lds1_addr = lds_address(lds1);
   auto copy = [&](int q, uint32_t stage) {
@@ -939,10 +973,10 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   };
 #pragma unroll
   for (int q = 0; q < NCOPY; ++q) copy(q, lds0_addr);
-  w.advance(p, nk, BK);
+  w.advance(nk);
 #pragma unroll
   for (int q = 0; q < NCOPY; ++q) copy(q, lds1_addr);
-  w.advance(p, nk, BK);
+  w.advance(nk);
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY) : "memory");  // K tile 0 of this wave landed
   __syncthreads();
   frags(lds0, 0, 0);
@@ -982,7 +1016,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
         else bf[0][r0 - FM] = *reinterpret_cast<const uint4*>(stage_nxt + bbase + kofs[0] + (r0 - FM) * 16 * BK);
       }
     }
-    w.advance(p, nk, BK);
+    w.advance(nk);
     __builtin_amdgcn_sched_barrier(0);
   };
   using First = std::integral_constant<bool, true>;
@@ -997,10 +1031,21 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   pipe_drain(acc);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  store_pipe<T, BN, FM, FN>(p, lds0, lds1, acc, m0, n0, boff_c);
+  if (p.bias != nullptr) store_pipe<T, BN, FM, FN, true>(p, lds0, lds1, acc, m0, n0, boff_c);
+  else store_pipe<T, BN, FM, FN, false>(p, lds0, lds1, acc, m0, n0, boff_c);
 }
 
 // ---- launcher ----------------------------------------------------------------------
+// contract_pipe keeps as many K walk levels as the descriptor has (1, 2, or up to 4)
+template <typename T, int BN>
+void launch_pipe(const ContractArgs& p, hipStream_t s) {
+  switch (p.klevels) {
+    case 1: contract_pipe<T, BN, 1><<<p.total_tiles, 256, 0, s>>>(p); break;
+    case 2: contract_pipe<T, BN, 2><<<p.total_tiles, 256, 0, s>>>(p); break;
+    default: contract_pipe<T, BN, kKLevels><<<p.total_tiles, 256, 0, s>>>(p); break;
+  }
+}
+
 template <typename T, int BM, int BN, int WM, int WN, int LA, int LB, int PF>
 int launch_one(const ContractArgs& p, hipStream_t s, const char* name) {
   contract_kernel<T, BM, BN, WM, WN, LA, LB, PF><<<p.total_tiles, WM * WN * 64, 0, s>>>(p);
@@ -1014,10 +1059,10 @@ int launch_layouts(const ContractArgs& p, int la, int lb, hipStream_t s, const c
     if constexpr (BM == 256 && BN == 256 && sizeof(typename Traits<T>::S) == 2) {
       if (!p.off32) return launch_one<T, BM, BN, WM, WN, kKContig, kKContig, PF>(p, s, name);
       if (p.pipe_bn == 224) {
-        contract_pipe<T, 224><<<p.total_tiles, 256, 0, s>>>(p);
+        launch_pipe<T, 224>(p, s);
         set_kernel("contract_pipe_256x224");
       } else {
-        contract_pipe<T, 256><<<p.total_tiles, 256, 0, s>>>(p);
+        launch_pipe<T, 256>(p, s);
         set_kernel("contract_pipe_256x256");
       }
       return check_launch("es_contract");
