@@ -199,8 +199,91 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(const GatherArgs p) {
   }
 }
 
+// ---- whole rows -------------------------------------------------------------------
+// When the innermost output dim is a plain contiguous run of the input (stride 1, no
+// offset, no range check, no window), an output row is one copy of a contiguous input
+// run.  Rows are cut into segments of one pass: 2^LPR lanes x kRowUnroll vectors.  A
+// segment's source is formed once (source_of at its first vector, with every boundary
+// rule) and its lanes move its vectors, lane i taking vectors i, i + 2^LPR, ...  With at
+// least 8 lanes per segment each access instruction touches whole 128-byte lines, and the
+// index arithmetic is paid once per kRowUnroll vectors instead of once per vector.
+// Consecutive waves take consecutive segments, so the waves in flight cover one
+// contiguous stretch of the output (long rows handed out whole would put every wave
+// at the same offset of its own row: addresses a row apart, which fall into the same
+// HBM channels).
+constexpr int kRowUnroll = 4;
+
+template <int VB, int R, typename OffT, int BOUNDARY, bool M24, bool NT>
+__global__ __launch_bounds__(kThreads) void gather_rows(const GatherArgs p, uint32_t units, uint32_t row_vecs,
+                                                        FastDiv segs, int lpr) {
+  using V = typename Vec<VB>::type;
+  const V fillv = fill_vec<VB>(p.fill);
+  const int lane = threadIdx.x % 64;
+  const uint32_t wave = blockIdx.x * (kThreads / 64) + threadIdx.x / 64;
+  const uint32_t waves = gridDim.x * (kThreads / 64);
+  const uint32_t per_wave = 64u >> lpr;  // segments a wave moves at once
+  const uint32_t li = uint32_t(lane) & ((1u << lpr) - 1);
+  const uint32_t seg_vecs = (1u << lpr) * kRowUnroll;
+  for (uint32_t unit = wave * per_wave + (uint32_t(lane) >> lpr); unit < units; unit += waves * per_wave) {
+    uint32_t seg;
+    const uint32_t row = segs.divmod(unit, seg);
+    const uint32_t first = seg * seg_vecs;  // the segment's first vector in its row
+    bool outside;
+    const OffT src = source_of<R, OffT, BOUNDARY, M24>(p, row * row_vecs + first, outside);
+    const V* in = reinterpret_cast<const V*>(p.x + (outside ? OffT(0) : src));
+    V* out = reinterpret_cast<V*>(p.out) + size_t(row) * row_vecs + first;
+    V value[kRowUnroll];
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const uint32_t v = li + (uint32_t(u) << lpr);
+      // a fill segment loads (and discards) offset 0, always valid
+      if (first + v < row_vecs) value[u] = NT ? load_nt(in + (outside ? 0 : v)) : in[outside ? 0 : v];
+    }
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const uint32_t v = li + (uint32_t(u) << lpr);
+      if (first + v < row_vecs) store_nt(out + v, outside ? fillv : value[u]);
+    }
+  }
+}
+
 // index arithmetic of a launch: 64-bit offsets, 32-bit, or 32-bit with 24-bit multiplies
 enum class Index { k64, k32, k24 };
+
+struct RowLaunch {
+  uint32_t units, row_vecs;
+  FastDiv segs;  // segments per row
+  int lpr;
+  uint32_t blocks;
+};
+
+template <int VB, typename OffT, int BOUNDARY, bool M24, bool NT>
+void launch_rows_rank(const GatherArgs& p, const RowLaunch& r, hipStream_t s) {
+  switch (p.out_rank) {
+    case 2:
+      gather_rows<VB, 2, OffT, BOUNDARY, M24, NT><<<r.blocks, kThreads, 0, s>>>(p, r.units, r.row_vecs, r.segs, r.lpr);
+      break;
+    case 4:
+      gather_rows<VB, 4, OffT, BOUNDARY, M24, NT><<<r.blocks, kThreads, 0, s>>>(p, r.units, r.row_vecs, r.segs, r.lpr);
+      break;
+    case 6:
+      gather_rows<VB, 6, OffT, BOUNDARY, M24, NT><<<r.blocks, kThreads, 0, s>>>(p, r.units, r.row_vecs, r.segs, r.lpr);
+      break;
+    default:
+      gather_rows<VB, 8, OffT, BOUNDARY, M24, NT><<<r.blocks, kThreads, 0, s>>>(p, r.units, r.row_vecs, r.segs, r.lpr);
+      break;
+  }
+}
+
+// 16-byte vectors only (the rows path is taken for rows of at least 16 of them)
+template <int BOUNDARY, bool NT>
+void launch_rows_index(const GatherArgs& p, Index index, const RowLaunch& r, hipStream_t s) {
+  switch (index) {
+    case Index::k64: launch_rows_rank<16, int64_t, BOUNDARY, false, NT>(p, r, s); break;
+    case Index::k32: launch_rows_rank<16, int32_t, BOUNDARY, false, NT>(p, r, s); break;
+    default: launch_rows_rank<16, int32_t, BOUNDARY, true, NT>(p, r, s); break;
+  }
+}
 
 template <int VB, typename OffT, int BOUNDARY, bool M24, bool NT = false>
 void launch_rank(const GatherArgs& p, uint32_t blocks, hipStream_t s) {
@@ -1108,6 +1191,49 @@ extern "C" int es_gather(const es_gather_desc* d, const void* x, void* out, void
   }
   for (int j = 0; j < d->in_rank && once; ++j)
     if (d->win[j] >= 0) once = false;
+  // whole rows: the innermost output dim a plain contiguous input run (its input dim
+  // unchecked, fed by no window) of 16 to 64 vectors.  Measured against the general
+  // kernel: 14 % faster on 512-byte rows with two wrapped dims (a roll), 3 % on a
+  // padded 512-byte-row copy; 10 % slower on 4 KB rows and 4 % on 64 KB rows, which the
+  // general kernel's XCD runs already stream well.
+  if (vb == 16 && total_vec < 0x80000000ull) {
+    int feeder = -1;
+    bool windowed = false;
+    for (int j = 0; j < d->in_rank; ++j) {
+      if (d->pos[j] == inner) feeder = j;
+      if (d->win[j] == inner) windowed = true;
+    }
+    const uint64_t row_vecs = uint64_t(d->out_size[inner]) / uint64_t(inner_scale);
+    if (feeder >= 0 && !windowed && !checked[feeder] && d->in_stride[feeder] == 1 && row_vecs >= 16 &&
+        row_vecs <= 64) {
+      RowLaunch r;
+      r.lpr = 3;  // at least 8 lanes (128 bytes) per segment
+      while (r.lpr < 6 && (uint64_t(1) << r.lpr) * kRowUnroll < row_vecs) ++r.lpr;
+      const uint64_t seg_vecs = (uint64_t(1) << r.lpr) * kRowUnroll;
+      const uint64_t segs = (row_vecs + seg_vecs - 1) / seg_vecs;
+      const uint64_t units = (total_vec / row_vecs) * segs;
+      if (units < 0x80000000ull) {
+        r.units = uint32_t(units);
+        r.row_vecs = uint32_t(row_vecs);
+        r.segs.init(uint32_t(segs));
+        const uint64_t waves = (units + (64u >> r.lpr) - 1) / (64u >> r.lpr);
+        const uint64_t rblocks = (waves + kThreads / 64 - 1) / (kThreads / 64);
+        r.blocks = uint32_t(rblocks > 1048576 ? 1048576 : rblocks);
+        static const char* const kRowNames[3] = {"gather_rows_o64", "gather_rows", "gather_rows_m24"};
+        if (once) {
+          launch_rows_index<ES_BOUNDARY_CONSTANT, true>(p, index, r, s);
+        } else {
+          switch (d->boundary) {
+            case ES_BOUNDARY_REPLICATE: launch_rows_index<ES_BOUNDARY_REPLICATE, false>(p, index, r, s); break;
+            case ES_BOUNDARY_PERIODIC: launch_rows_index<ES_BOUNDARY_PERIODIC, false>(p, index, r, s); break;
+            default: launch_rows_index<ES_BOUNDARY_CONSTANT, false>(p, index, r, s); break;
+          }
+        }
+        set_kernel(kRowNames[int(index)]);
+        return check_launch("es_gather");
+      }
+    }
+  }
   switch (vb) {
     case 16:
       if (once) launch_stream16(p, index, blocks, s);
