@@ -395,3 +395,40 @@ def test_transposes_with_short_or_odd_dims(gpu, shape):
     for dtype in (torch.uint8, torch.bfloat16, torch.float32):
         x = (randn(*shape, seed=82) * 50).to(dtype)
         assert_bitexact(es.einshard("a p q -> a q p", x.to(gpu)), einshard_cpu("a p q -> a q p", x))
+
+
+@pytest.mark.parametrize(
+    "batch, m, n, k",
+    [
+        (1, 4096, 4136, 128),  # ragged N
+        (4, 2048, 2000, 192),  # batched, ragged N, three 64-deep K tiles
+        (1, 4104, 4096, 256),  # ragged M (a multiple of 8)
+        (1, 4100, 4096, 128),  # M not a multiple of 8: element stores
+    ],
+)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bias", [False, True])
+def test_output_contiguous_along_m(gpu, batch, m, n, k, dtype, bias):
+    # out[b, n, m] = sum_k x[b, m, k] y[b, n, k] with M the A operand: the output is
+    # contiguous along the tile's rows, so contract_pipe stages the tile transposed
+    from torch_einshard._exec import launch, prepare_op
+    from torch_einshard.planner import ContractOp, SubAxis
+
+    x = randn(batch, m, k, seed=91, dtype=dtype)
+    y = randn(batch, n, k, seed=92, dtype=dtype)
+    b = randn(n, seed=93, dtype=dtype) if bias else None
+    op = ContractOp(
+        (batch, n, m),
+        swapped=False,
+        batch=[SubAxis(batch, a=m * k, b=n * k, c=n * m)],
+        m=[SubAxis(m, a=k, c=1)],
+        n=[SubAxis(n, b=k, c=m)],
+        k=[SubAxis(k, a=1, b=1)],
+    )
+    prep = prepare_op(op, dtype, 2)
+    got = launch(prep, (x.to(gpu), y.to(gpu)), gpu, dtype, bias=None if b is None else b.to(gpu))
+    assert _native.last_kernel().startswith("contract_pipe"), _native.last_kernel()
+    want = torch.matmul(y.float(), x.float().transpose(1, 2))  # [b, n, m]
+    if b is not None:
+        want = want + b.float()[None, :, None]
+    assert_rel(got, want.to(dtype), TOL[dtype])

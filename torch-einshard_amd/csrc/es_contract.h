@@ -66,7 +66,7 @@ struct ContractArgs {
   uint32_t group_n;      // N-tiles per tile group (divides tiles_n; see tile_of)
   uint32_t total_tiles;
   uint32_t pipe_bn;      // 224: contract_pipe's 256 x 224 tiles; 0: 256 x 256
-  int32_t vstore;        // 16-byte vector stores along n
+  int32_t vstore;        // 16-byte vector stores: 1 along n; 2 along m (contract_pipe only)
   int32_t off32;         // every byte offset into A and B fits in 32 bits
   int64_t ka_inner;      // stride of the innermost K sub-axis in A
   int64_t kb_inner;      // ... in B

@@ -177,6 +177,13 @@ int contract(const es_contract_desc* d, const void* a, const void* b, const void
         strides_multiple(d->m, d->n_m, 0, 2, vec) && strides_multiple(d->batch, d->n_batch, 0, 2, vec))
       p.vstore = 1;
   }
+  // the output contiguous along M instead (contract_pipe stages the tile transposed)
+  if (p.vstore == 0 && esz == 2 && d->n_m > 0) {
+    const es_axis& min_ = d->m[d->n_m - 1];
+    if (min_.c == 1 && min_.size % vec == 0 && aligned(c, 16) && strides_multiple(d->m, d->n_m, 1, 2, vec) &&
+        strides_multiple(d->n, d->n_n, 0, 2, vec) && strides_multiple(d->batch, d->n_batch, 0, 2, vec))
+      p.vstore = 2;
+  }
 
   // tile: the largest that still gives every CU a tile of its own
   static const int tile_of[3] = {256, 128, 64};

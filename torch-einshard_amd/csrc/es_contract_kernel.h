@@ -469,7 +469,7 @@ __device__ __forceinline__ void store_tile(const ContractArgs& p, void* lds, con
     }
     lds_barrier();
     // staged row r is tile row (r / 32) * WTM + i * 32 + r % 32
-    if (p.vstore) {
+    if (p.vstore == 1) {
       constexpr int CV = BN / VEC;  // vectors per staged row
       for (int v = tid; v < SROWS * CV; v += NT) {
         const int r = v / CV;
@@ -873,7 +873,7 @@ __device__ __forceinline__ void store_pipe(const ContractArgs& p, typename Trait
       }
     lds_barrier();
     // staged row rr of stage h is tile row h * 128 + q * RR + rr
-    if (p.vstore) {
+    if (p.vstore == 1) {
       constexpr int CV = BN / VEC;  // vectors per row
       for (int v = tid; v < 2 * RR * CV; v += NT) {
         const int h = v / (RR * CV);
@@ -897,6 +897,82 @@ __device__ __forceinline__ void store_pipe(const ContractArgs& p, typename Trait
         const int64_t co = col_off[cn];
         if (ro >= 0 && co >= 0) C[ro + co] = (h ? lds1 : lds0)[rr * SLD + cn];
       }
+    }
+    if (q + 1 < P) lds_barrier();
+  }
+}
+
+// The epilogue of contract_pipe when the output is contiguous along the tile's rows
+// (the innermost M sub-axis, ContractArgs::vstore == 2): the tile is staged transposed,
+// [column n][row m], and written with 16-byte streaming stores along m.  A lane's four
+// consecutive-n values go to four staged rows (four 2-byte LDS writes).  Passes and
+// tables as in store_pipe, sized for the transposed stage.
+template <typename T, int BN, int FM, int FN, bool BIAS>
+__device__ __forceinline__ void store_pipe_t(const ContractArgs& p, typename Traits<T>::S* lds0,
+                                             typename Traits<T>::S* lds1, const f32x4 (&acc)[FM][FN], uint32_t m0,
+                                             uint32_t n0, int64_t boff_c) {
+  using S = typename Traits<T>::S;
+  constexpr int BM = 256, WTN = BN / 2, VEC = 8, NT = 256;
+  constexpr int STAGE_BYTES = (BM + BN) * kRowBytes;
+  constexpr int TABLES = BM * 8;
+  constexpr int P = BN * (16 * FM + VEC) * int(sizeof(S)) + TABLES <= STAGE_BYTES ? 1 : 2;  // passes
+  constexpr int BPP = FM / P;        // 16-row blocks per wave row per pass
+  constexpr int RR = 16 * BPP;       // rows per stage per pass
+  constexpr int SLM = RR + VEC;      // staging pitch (elements) of a column
+  constexpr int MV = RR / VEC;       // 16-byte vectors per staged column
+  static_assert(FM % P == 0 && BN * SLM * int(sizeof(S)) + TABLES <= STAGE_BYTES, "epilogue fits the stages");
+  int64_t* row_off = reinterpret_cast<int64_t*>(reinterpret_cast<char*>(lds0) + BN * SLM * int(sizeof(S)));
+  int64_t* col_off = reinterpret_cast<int64_t*>(reinterpret_cast<char*>(lds1) + BN * SLM * int(sizeof(S)));
+  const int tid = threadIdx.x;
+  const int lane = tid % 64;
+  const int wave = tid / 64;
+  const int wm = wave / 2;
+  const int wn = wave % 2;
+  S* region = wm == 0 ? lds0 : lds1;
+  S* C = static_cast<S*>(p.c);
+  const KArgs kp = kernel_args();
+  for (int r = tid; r < BM; r += NT) {
+    const uint32_t m = m0 + r;
+    row_off[r] = m < p.M ? boff_c + group_offset_k<2>(&kp->gm, m) : -1;
+  }
+  for (int c = tid; c < BN; c += NT) {
+    const uint32_t n = n0 + c;
+    col_off[c] = n < p.N ? group_offset_k<2>(&kp->gn, n) : -1;
+  }
+  f32x4 bv[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t n = n0 + wn * WTN + j * 16 + 4 * (lane / 16) + r;
+      bv[j][r] = BIAS && n < p.N ? Elem<T>::load(static_cast<const S*>(p.bias)[n]) : 0.f;
+    }
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+#pragma unroll
+    for (int ii = 0; ii < BPP; ++ii)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const f32x4 a = BIAS ? acc[q * BPP + ii][j] + bv[j] : acc[q * BPP + ii][j];
+        const uint32_t lo = Traits<T>::pack2(a[0], a[1]), hi = Traits<T>::pack2(a[2], a[3]);
+        S* col = region + (wn * WTN + j * 16 + 4 * (lane / 16)) * SLM + ii * 16 + lane % 16;
+        col[0] = S(lo);
+        col[SLM] = S(lo >> 16);
+        col[2 * SLM] = S(hi);
+        col[3 * SLM] = S(hi >> 16);
+      }
+    lds_barrier();
+    // staged column c of stage h holds tile rows h * 128 + q * RR + (0 .. RR) of column c
+    for (int v = tid; v < 2 * BN * MV; v += NT) {
+      const int h = v / (BN * MV);
+      const int rem = v - h * (BN * MV);
+      const int c = rem / MV;
+      const int mv = rem - c * MV;
+      const int64_t ro = row_off[h * 128 + q * RR + mv * VEC];
+      const int64_t co = col_off[c];
+      if (ro >= 0 && co >= 0)
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>((h ? lds1 : lds0) + c * SLM + mv * VEC),
+                                    reinterpret_cast<u32x4*>(C + ro + co));
     }
     if (q + 1 < P) lds_barrier();
   }
@@ -1031,8 +1107,13 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   pipe_drain(acc);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (p.bias != nullptr) store_pipe<T, BN, FM, FN, true>(p, lds0, lds1, acc, m0, n0, boff_c);
-  else store_pipe<T, BN, FM, FN, false>(p, lds0, lds1, acc, m0, n0, boff_c);
+  if (p.vstore == 2) {
+    if (p.bias != nullptr) store_pipe_t<T, BN, FM, FN, true>(p, lds0, lds1, acc, m0, n0, boff_c);
+    else store_pipe_t<T, BN, FM, FN, false>(p, lds0, lds1, acc, m0, n0, boff_c);
+  } else {
+    if (p.bias != nullptr) store_pipe<T, BN, FM, FN, true>(p, lds0, lds1, acc, m0, n0, boff_c);
+    else store_pipe<T, BN, FM, FN, false>(p, lds0, lds1, acc, m0, n0, boff_c);
+  }
 }
 
 // ---- launcher ----------------------------------------------------------------------
