@@ -371,14 +371,25 @@ __global__ __launch_bounds__(256) void transpose_kernel(const TransposeArgs a) {
       out_base += int64_t(r) * a.rest_out[d];
     }
     const uint32_t p0 = tp * TP, q0 = tq * kTileQ;
-    // read: vectors along P, one row of the tile per q
+    // read: vectors along P, one row of the tile per q; all of a lane's loads are issued
+    // before the first LDS write
     constexpr int RV = TP / VEC;  // vectors per q row
-    for (int v = threadIdx.x; v < kTileQ * RV; v += 256) {
-      const int q = v / RV, pv = (v - q * RV) * VEC;
-      if (p0 + pv < a.size_p && q0 + q < a.size_q) {
-        const V val = load_nt(reinterpret_cast<const V*>(x + in_base + int64_t(q0 + q) * a.q_in_stride + p0 + pv));
+    constexpr int RN = (kTileQ * RV + 255) / 256;
+    V val[RN];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) tile[q][pv + e] = val.v[e];
+    for (int i = 0; i < RN; ++i) {
+      const int v = threadIdx.x + i * 256;
+      const int q = v / RV, pv = (v - q * RV) * VEC;
+      if (v < kTileQ * RV && p0 + pv < a.size_p && q0 + q < a.size_q)
+        val[i] = load_nt(reinterpret_cast<const V*>(x + in_base + int64_t(q0 + q) * a.q_in_stride + p0 + pv));
+    }
+#pragma unroll
+    for (int i = 0; i < RN; ++i) {
+      const int v = threadIdx.x + i * 256;
+      const int q = v / RV, pv = (v - q * RV) * VEC;
+      if (v < kTileQ * RV && p0 + pv < a.size_p && q0 + q < a.size_q) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) tile[q][pv + e] = val[i].v[e];
       }
     }
     __syncthreads();
@@ -488,6 +499,216 @@ bool try_transpose(const es_gather_desc* d, const void* x, void* out, hipStream_
       break;
   }
   set_kernel("gather_transpose");
+  status = check_launch("es_gather");
+  return true;
+}
+
+// ---- padded transposes --------------------------------------------------------------
+// The same tile transpose when some dims carry an offset (a halo, a roll): input
+// coordinate = output coordinate + offset, out-of-range coordinates take the boundary
+// rule.  Reads are single elements along P (64 lanes cover 64 consecutive input
+// elements) because an offset along P breaks vector alignment; writes are WVEC-element
+// vectors along Q as in transpose_kernel.  The outer dims' coordinates are resolved once
+// per tile.  (A transposing halo is what a channels-first input needs before a
+// channels-last convolution.)
+struct TransposePadArgs {
+  const unsigned char* x;
+  unsigned char* out;
+  uint64_t fill;  // fill bits of one element
+  uint32_t tiles_p, tiles_q, n_outer;
+  uint32_t size_p, size_q;  // output extents of P and Q
+  int32_t in_p, in_q;       // input extents of the dims feeding P and Q
+  int32_t off_p, off_q;     // input coordinate = output coordinate + offset
+  int64_t q_in_stride;      // elements (P's input stride is 1)
+  int64_t p_out_stride;     // elements (output is dense)
+  int32_t n_rest;           // other output dims, outermost first
+  FastDiv rest_div[kMax];
+  int64_t rest_in[kMax];    // input stride of each (elements)
+  int64_t rest_out[kMax];   // output stride of each (elements)
+  int32_t rest_size[kMax];  // input extent of each
+  int32_t rest_off[kMax];   // offset of each
+};
+
+// input coordinate i of an extent-n dim under the boundary rule; a constant boundary
+// only flags the element
+template <int BOUNDARY>
+__device__ __forceinline__ int32_t bound_coord(int32_t i, int32_t n, bool& outside) {
+  if (uint32_t(i) < uint32_t(n)) return i;
+  if constexpr (BOUNDARY == ES_BOUNDARY_CONSTANT) {
+    outside = true;
+    return 0;
+  } else if constexpr (BOUNDARY == ES_BOUNDARY_REPLICATE) {
+    return i < 0 ? 0 : n - 1;
+  } else {
+    const int32_t r = i % n;
+    return r < 0 ? r + n : r;
+  }
+}
+
+template <typename E, int WVEC, int TP, int BOUNDARY>
+__global__ __launch_bounds__(256) void transpose_pad_kernel(const TransposePadArgs a) {
+  using V = EVec<E, WVEC>;
+  __shared__ E tile[kTileQ][TP + 1];
+  const E* x = reinterpret_cast<const E*>(a.x);
+  E* out = reinterpret_cast<E*>(a.out);
+  const E fill = E(a.fill);
+  const uint32_t per_outer = a.tiles_p * a.tiles_q;
+  for (uint32_t b = blockIdx.x; b < per_outer * a.n_outer; b += gridDim.x) {
+    uint32_t outer = b / per_outer;
+    const uint32_t t = b - outer * per_outer;
+    const uint32_t tp = t / a.tiles_q, tq = t - tp * a.tiles_q;
+    int64_t in_base = 0, out_base = 0;
+    bool rest_outside = false;
+    for (int d = a.n_rest - 1; d >= 0; --d) {
+      uint32_t r;
+      outer = a.rest_div[d].divmod(outer, r);
+      const int32_t i = bound_coord<BOUNDARY>(int32_t(r) + a.rest_off[d], a.rest_size[d], rest_outside);
+      in_base += int64_t(i) * a.rest_in[d];
+      out_base += int64_t(r) * a.rest_out[d];
+    }
+    const uint32_t p0 = tp * TP, q0 = tq * kTileQ;
+    // read: one element per lane, consecutive lanes along P; all of a lane's loads are
+    // issued before the first LDS write, so they are in flight together
+    constexpr int RN = kTileQ * TP / 256;
+    E val[RN];
+#pragma unroll
+    for (int i = 0; i < RN; ++i) {
+      const int v = threadIdx.x + i * 256;
+      const int q = v / TP, p = v - q * TP;
+      bool outside = rest_outside || p0 + p >= a.size_p || q0 + q >= a.size_q;
+      const int32_t ip = bound_coord<BOUNDARY>(int32_t(p0 + p) + a.off_p, a.in_p, outside);
+      const int32_t iq = bound_coord<BOUNDARY>(int32_t(q0 + q) + a.off_q, a.in_q, outside);
+      val[i] = outside ? fill : x[in_base + int64_t(iq) * a.q_in_stride + ip];
+    }
+#pragma unroll
+    for (int i = 0; i < RN; ++i) {
+      const int v = threadIdx.x + i * 256;
+      tile[v / TP][v % TP] = val[i];
+    }
+    __syncthreads();
+    // write: vectors along Q, one output row per p
+    constexpr int WV = kTileQ / WVEC;
+    for (int v = threadIdx.x; v < TP * WV; v += 256) {
+      const int p = v / WV, qv = (v - p * WV) * WVEC;
+      if (p0 + p < a.size_p && q0 + qv < a.size_q) {
+        V val;
+#pragma unroll
+        for (int e = 0; e < WVEC; ++e) val.v[e] = tile[qv + e][p];
+        store_nt(reinterpret_cast<V*>(out + out_base + int64_t(p0 + p) * a.p_out_stride + q0 + qv), val);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <typename E, int WVEC, int BOUNDARY>
+void launch_transpose_pad_tp(const TransposePadArgs& a, int tp, uint32_t blocks, hipStream_t s) {
+  switch (tp) {
+    case 8: transpose_pad_kernel<E, WVEC, 8, BOUNDARY><<<blocks, 256, 0, s>>>(a); break;
+    case 16: transpose_pad_kernel<E, WVEC, 16, BOUNDARY><<<blocks, 256, 0, s>>>(a); break;
+    case 32: transpose_pad_kernel<E, WVEC, 32, BOUNDARY><<<blocks, 256, 0, s>>>(a); break;
+    default: transpose_pad_kernel<E, WVEC, 64, BOUNDARY><<<blocks, 256, 0, s>>>(a); break;
+  }
+}
+
+template <typename E, int WIDE>
+void launch_transpose_pad(const TransposePadArgs& a, bool wide, int boundary, int tp, uint32_t blocks, hipStream_t s) {
+  switch (boundary) {
+    case ES_BOUNDARY_REPLICATE:
+      if (wide) launch_transpose_pad_tp<E, WIDE, ES_BOUNDARY_REPLICATE>(a, tp, blocks, s);
+      else launch_transpose_pad_tp<E, 1, ES_BOUNDARY_REPLICATE>(a, tp, blocks, s);
+      break;
+    case ES_BOUNDARY_PERIODIC:
+      if (wide) launch_transpose_pad_tp<E, WIDE, ES_BOUNDARY_PERIODIC>(a, tp, blocks, s);
+      else launch_transpose_pad_tp<E, 1, ES_BOUNDARY_PERIODIC>(a, tp, blocks, s);
+      break;
+    default:
+      if (wide) launch_transpose_pad_tp<E, WIDE, ES_BOUNDARY_CONSTANT>(a, tp, blocks, s);
+      else launch_transpose_pad_tp<E, 1, ES_BOUNDARY_CONSTANT>(a, tp, blocks, s);
+      break;
+  }
+}
+
+// The padded-transpose path of es_gather: every input dim feeds one output dim through
+// `pos` (no window), the input's unit-stride dim feeds an output dim P other than the
+// innermost one Q, and some dim has an offset or a different extent.
+bool try_transpose_pad(const es_gather_desc* d, const void* x, void* out, hipStream_t s, int& status) {
+  const int rank = d->out_rank;
+  if (d->in_rank != rank || rank < 2) return false;
+  int feeder[kMax];
+  for (int i = 0; i < rank; ++i) feeder[i] = -1;
+  bool padded = false;
+  for (int j = 0; j < rank; ++j) {
+    const int p = d->pos[j];
+    if (d->win[j] >= 0 || feeder[p] >= 0 || d->in_size[j] <= 0) return false;
+    if (d->in_size[j] >= (int64_t(1) << 30) || d->out_size[p] >= (int64_t(1) << 30)) return false;
+    if (d->offset[j] <= -(int64_t(1) << 30) || d->offset[j] >= (int64_t(1) << 30)) return false;
+    if (d->offset[j] != 0 || d->in_size[j] != d->out_size[p]) padded = true;
+    feeder[p] = j;
+  }
+  if (!padded) return false;
+  const int q = rank - 1;
+  int pdim = -1;
+  for (int i = 0; i < rank - 1; ++i)
+    if (d->in_stride[feeder[i]] == 1 && d->out_size[i] > 1) pdim = i;
+  if (pdim < 0 || d->in_stride[feeder[q]] == 1 || d->out_size[q] < kTileQ / 4) return false;
+  TransposePadArgs a;
+  a.x = static_cast<const unsigned char*>(x);
+  a.out = static_cast<unsigned char*>(out);
+  const int es_ = d->elem_size;
+  a.fill = es_ < 8 ? (d->fill_bits & ((uint64_t(1) << (8 * es_)) - 1)) : d->fill_bits;
+  a.size_p = uint32_t(d->out_size[pdim]);
+  a.size_q = uint32_t(d->out_size[q]);
+  a.in_p = int32_t(d->in_size[feeder[pdim]]);
+  a.in_q = int32_t(d->in_size[feeder[q]]);
+  a.off_p = int32_t(d->offset[feeder[pdim]]);
+  a.off_q = int32_t(d->offset[feeder[q]]);
+  a.tiles_q = (a.size_q + kTileQ - 1) / kTileQ;
+  a.q_in_stride = d->in_stride[feeder[q]];
+  int64_t dense[kMax];
+  int64_t run = 1;
+  for (int i = rank - 1; i >= 0; --i) {
+    dense[i] = run;
+    run *= d->out_size[i];
+  }
+  a.p_out_stride = dense[pdim];
+  a.n_rest = 0;
+  uint64_t n_outer = 1;
+  for (int i = 0; i < rank; ++i) {
+    if (i == pdim || i == q) continue;
+    a.rest_div[a.n_rest].init(uint32_t(d->out_size[i]));
+    a.rest_in[a.n_rest] = d->in_stride[feeder[i]];
+    a.rest_out[a.n_rest] = dense[i];
+    a.rest_size[a.n_rest] = int32_t(d->in_size[feeder[i]]);
+    a.rest_off[a.n_rest] = int32_t(d->offset[feeder[i]]);
+    n_outer *= uint64_t(d->out_size[i]);
+    ++a.n_rest;
+  }
+  for (int i = a.n_rest; i < kMax; ++i) {
+    a.rest_div[i].init(1);
+    a.rest_in[i] = a.rest_out[i] = 0;
+    a.rest_size[i] = 1;
+    a.rest_off[i] = 0;
+  }
+  // 16-byte writes along Q when every vector is aligned and whole
+  const int vec = 16 / es_;
+  bool wide = aligned(out, 16) && a.size_q % vec == 0 && (a.p_out_stride * es_) % 16 == 0;
+  for (int i = 0; i < a.n_rest && wide; ++i)
+    if ((a.rest_out[i] * es_) % 16 != 0) wide = false;
+  int tp = 8;
+  while (tp < 64 && uint32_t(tp) < a.size_p) tp *= 2;
+  a.tiles_p = (a.size_p + tp - 1) / tp;
+  const uint64_t blocks64 = n_outer * a.tiles_p * a.tiles_q;
+  if (blocks64 > kU32Max) return false;
+  a.n_outer = uint32_t(n_outer);
+  const uint32_t blocks = uint32_t(blocks64 > 1048576 ? 1048576 : blocks64);
+  switch (es_) {
+    case 1: launch_transpose_pad<uint8_t, 16>(a, wide, d->boundary, tp, blocks, s); break;
+    case 2: launch_transpose_pad<uint16_t, 8>(a, wide, d->boundary, tp, blocks, s); break;
+    case 4: launch_transpose_pad<uint32_t, 4>(a, wide, d->boundary, tp, blocks, s); break;
+    default: launch_transpose_pad<uint64_t, 2>(a, wide, d->boundary, tp, blocks, s); break;
+  }
+  set_kernel("gather_transpose_pad");
   status = check_launch("es_gather");
   return true;
 }
@@ -1037,6 +1258,7 @@ extern "C" int es_gather(const es_gather_desc* d, const void* x, void* out, void
   {
     int status = ES_OK;
     if (try_transpose(d, x, out, static_cast<hipStream_t>(stream), status)) return status;
+    if (try_transpose_pad(d, x, out, static_cast<hipStream_t>(stream), status)) return status;
   }
 
   // widest vector: the innermost output dim must feed exactly one input dim,
