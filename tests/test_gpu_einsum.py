@@ -432,3 +432,21 @@ def test_output_contiguous_along_m(gpu, batch, m, n, k, dtype, bias):
     if b is not None:
         want = want + b.float()[None, :, None]
     assert_rel(got, want.to(dtype), TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m, n, k", [(256, 512, 16384), (100, 300, 9000), (64, 64, 65536)])
+def test_split_k(gpu, m, n, k, dtype):
+    # few output tiles and a long K: partial contractions over parts of K, then their sum
+    from torch_einshard._exec import _split_k
+    from torch_einshard.planner import ContractOp, SubAxis
+
+    _, parts = _split_k(ContractOp((m, n), swapped=False, m=[SubAxis(m, a=1, c=n)], n=[SubAxis(n, b=1, c=1)],
+                                   k=[SubAxis(k, a=m, b=n)]))
+    assert parts > 1
+    x = randn(k, m, seed=95, dtype=dtype)
+    y = randn(k, n, seed=96, dtype=dtype)
+    got = es.einshard("k m, k n -> m n", x.to(gpu), y.to(gpu))
+    assert _native.last_kernel().startswith("reduce"), _native.last_kernel()
+    want = einshard_cpu("k m, k n -> m n", x.float(), y.float())
+    assert_rel(got, want.to(dtype), TOL[dtype])

@@ -15,7 +15,7 @@ import torch
 
 from . import _native
 from ._native import MAX_AXES, BcastDesc, ContractDesc, GatherDesc, ReduceDesc, call
-from .planner import BcastOp, ContractOp, EmptyOp, GatherOp, ReduceOp, dense_strides
+from .planner import BcastOp, ContractOp, EmptyOp, GatherOp, ReduceOp, SubAxis, dense_strides
 
 __all__ = ["check_device_tensors", "run_op", "run_gather", "dtype_code", "fill_bits", "Prepared", "prepare_op", "launch"]
 
@@ -73,11 +73,15 @@ class Prepared:
     pointers, so a repeated expression costs one ctypes call on the host.
 
     ``repack`` lists operands first copied into a dense temporary by es_gather:
-    (operand index, gather descriptor, temporary shape)."""
+    (operand index, gather descriptor, temporary shape).
 
-    __slots__ = ("entry", "desc", "ref", "out_shape", "order", "workspace", "noop", "repack")
+    ``split`` (a split-K contraction): (partials, reduce descriptor, its workspace
+    bytes).  The contraction writes ``partials`` stacked partial results, which one
+    es_reduce sums into the output."""
 
-    def __init__(self, entry, desc, out_shape, order, workspace=0, noop=False, repack=()):
+    __slots__ = ("entry", "desc", "ref", "out_shape", "order", "workspace", "noop", "repack", "split")
+
+    def __init__(self, entry, desc, out_shape, order, workspace=0, noop=False, repack=(), split=None):
         self.entry = entry
         self.desc = desc
         self.ref = ctypes.byref(desc) if desc is not None else None
@@ -86,6 +90,7 @@ class Prepared:
         self.workspace = workspace
         self.noop = noop
         self.repack = tuple((index, desc_, ctypes.byref(desc_), shape) for index, desc_, shape in repack)
+        self.split = None if split is None else (split[0], split[1], ctypes.byref(split[1]), split[2])
 
 
 def _raw_stream(device):
@@ -112,6 +117,21 @@ def launch(prep, xs, device, dtype, bias=None):
                 raise _native.NativeError("es_gather", status, handle.es_last_error().decode())
             xs[index] = tmp
     ptrs = [xs[i].data_ptr() for i in prep.order]
+    if prep.split is not None:
+        # split-K: partial results, then their sum (a fixed order: deterministic)
+        if bias is not None:
+            raise AssertionError("a split-K contraction takes no bias")
+        partials, _, rref, need = prep.split
+        tmp = torch.empty((partials, out.numel()), dtype=dtype, device=device)
+        status = fn(prep.ref, *ptrs, tmp.data_ptr(), stream)
+        if status < 0:
+            raise _native.NativeError(prep.entry, status, handle.es_last_error().decode())
+        ws = torch.empty(need, dtype=torch.uint8, device=device) if need > 0 else None
+        status = handle.es_reduce(rref, tmp.data_ptr(), tmp.data_ptr(), out.data_ptr(),
+                                  ws.data_ptr() if ws is not None else None, need, stream)
+        if status < 0:
+            raise _native.NativeError("es_reduce", status, handle.es_last_error().decode())
+        return out
     if prep.entry == "es_reduce":
         need = prep.workspace
         ws = torch.empty(need, dtype=torch.uint8, device=device) if need > 0 else None
@@ -198,8 +218,46 @@ def _repack_for_k_contiguity(op, order, elem_size):
     return op, tuple(repack)
 
 
-def prepare_op(op, dtype, elem_size):
-    """Build the descriptor of a planner op for operands of ``dtype``."""
+# Split-K: a contraction with few output tiles and a long K leaves most CUs idle (a
+# weight gradient: out channels x kernel taps, summed over every position of a batch).
+# Its outermost K sub-axis is then cut into S parts that run as S more batch entries,
+# writing S stacked partial results; one es_reduce (over a leading axis, a fixed order)
+# adds them.  Partials are rounded to the output dtype, one rounding more than a
+# single pass.
+_SPLIT_TILE = 128       # tile edge the count below is taken at
+_SPLIT_BELOW = 128      # split when fewer output tiles than this ...
+_SPLIT_MIN_K = 8192     # ... and K is at least this long
+_SPLIT_TARGET = 256     # aim for this many tiles
+_SPLIT_K_PART = 512     # and keep at least this much K in each part
+
+
+def _split_k(op):
+    """(op with a leading split batch axis, partial count) or (op, 1)."""
+    if not op.k or not op.m or not op.n:
+        return op, 1
+    tiles = _prod(a.size for a in op.batch)
+    tiles *= -(-_prod(a.size for a in op.m) // _SPLIT_TILE) * -(-_prod(a.size for a in op.n) // _SPLIT_TILE)
+    k_total = _prod(a.size for a in op.k)
+    if tiles >= _SPLIT_BELOW or k_total < _SPLIT_MIN_K:
+        return op, 1
+    outer = op.k[0]
+    want = -(-_SPLIT_TARGET // tiles)
+    best = 1
+    for d in range(2, outer.size + 1):
+        if outer.size % d == 0 and d <= want and k_total // d >= _SPLIT_K_PART:
+            best = d
+    if best == 1:
+        return op, 1
+    out_numel = _prod(op.out_shape)
+    rest = outer.size // best
+    split_axis = SubAxis(best, a=outer.a * rest, b=outer.b * rest, c=out_numel, label="split")
+    k = ([SubAxis(rest, a=outer.a, b=outer.b, label=outer.label)] if rest > 1 else []) + list(op.k[1:])
+    return replace(op, out_shape=(best,) + tuple(op.out_shape), batch=[split_axis] + list(op.batch), k=k), best
+
+
+def prepare_op(op, dtype, elem_size, split=True):
+    """Build the descriptor of a planner op for operands of ``dtype`` (``split``: a
+    contraction with few tiles and a long K may run as split-K)."""
     if isinstance(op, EmptyOp) or any(size == 0 for size in op.out_shape):
         # nothing to compute: an empty output of any dtype, like torch.einsum
         return Prepared(None, None, op.out_shape, (), noop=True)
@@ -250,13 +308,26 @@ def prepare_op(op, dtype, elem_size):
     if isinstance(op, ContractOp):
         order = (1, 0) if op.swapped else (0, 1)
         op, repack = _repack_for_k_contiguity(op, order, elem_size)
+        out_shape = op.out_shape
+        parts = 1
+        if split:
+            op, parts = _split_k(op)
         desc = ContractDesc()
         desc.dtype = code
         desc.n_batch = _set_axes(desc.batch, op.batch, "einshard")
         desc.n_m = _set_axes(desc.m, op.m, "einshard")
         desc.n_n = _set_axes(desc.n, op.n, "einshard")
         desc.n_k = _set_axes(desc.k, op.k, "einshard")
-        return Prepared("es_contract", desc, op.out_shape, order, repack=repack)
+        if parts == 1:
+            return Prepared("es_contract", desc, out_shape, order, repack=repack)
+        numel = _prod(out_shape)
+        rdesc = ReduceDesc()
+        rdesc.dtype = code
+        rdesc.has_y = 0
+        rdesc.n_keep = _set_axes(rdesc.keep, [SubAxis(numel, a=1)], "einshard")
+        rdesc.n_red = _set_axes(rdesc.red, [SubAxis(parts, a=numel)], "einshard")
+        need = int(call("es_reduce_workspace_bytes", ctypes.byref(rdesc)))
+        return Prepared("es_contract", desc, out_shape, order, repack=repack, split=(parts, rdesc, need))
 
     raise TypeError(f"unknown planned op {type(op).__name__}")
 

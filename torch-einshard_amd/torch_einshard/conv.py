@@ -113,10 +113,11 @@ def _conv_op(xp, wk, dilation, out_order):
     return op, out_shape
 
 
-def _conv_prepare(xp, wk, dilation, out_order):
-    """The prepared contraction of one implicit-GEMM convolution."""
+def _conv_prepare(xp, wk, dilation, out_order, bias=False):
+    """The prepared contraction of one implicit-GEMM convolution (with a bias it never
+    runs as split-K: every partial would add it)."""
     op, _ = _conv_op(xp, wk, dilation, out_order)
-    return prepare_op(op, xp.dtype, xp.element_size())
+    return prepare_op(op, xp.dtype, xp.element_size(), split=not bias)
 
 
 def _conv_launch(prep, xp, wk, bias):
@@ -128,7 +129,7 @@ def _conv_launch(prep, xp, wk, bias):
 def _conv(xp, wk, bias, dilation, out_order):
     """Run one implicit-GEMM convolution (no autograd)."""
     check_device_tensors([xp, wk] + ([] if bias is None else [bias]), what="einconv")
-    return _conv_launch(_conv_prepare(xp, wk, dilation, out_order), xp, wk, bias)
+    return _conv_launch(_conv_prepare(xp, wk, dilation, out_order, bias is not None), xp, wk, bias)
 
 
 def _weight_grad(gz, xp, dilation, out_order, w_shape):
@@ -425,7 +426,7 @@ def einconv(
         if checkpoint not in _MODES:
             raise ValueError("checkpoint must be one of 'full', 'conv', 'none', True, or False")
         xp, wk, prep_x, prep_w = operands(x, weight, bias)
-        prep_c = _conv_prepare(xp, wk, geometry[0], geometry[1])
+        prep_c = _conv_prepare(xp, wk, geometry[0], geometry[1], bias is not None)
         out = _conv_launch(prep_c, xp, wk, bias)
         if key is not None:
             remember(key, (prep_x, prep_w, prep_c))
