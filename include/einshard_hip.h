@@ -84,8 +84,9 @@ typedef struct {
   int32_t win[ES_MAX_AXES];
 } es_gather_desc;
 
-/* Replaces: torch.einsum unary permutation/diagonal (einsum.py:132) and
- * _pad_dim + unfold + permute().contiguous() (halo.py:27-55, 402-418). */
+/* Replaces: torch.einsum unary permutation/diagonal (einsum.py:132),
+ * _pad_dim + unfold + permute().contiguous() (halo.py:27-55, 402-418) and
+ * torch.roll per axis (roll.py:27: offset -(shift mod n) with ES_BOUNDARY_PERIODIC). */
 int es_gather(const es_gather_desc* desc, const void* x, void* out, void* stream);
 
 /* ---- broadcast elementwise: out = x * y -------------------------------------

@@ -201,3 +201,60 @@ def test_zero_sized_operands():
     op = lower_einsum([list("ab"), list("bc")], [(20, 0), (0, 24)], [(1, 1), (24, 1)], list("ac"))
     assert isinstance(op, ContractOp) and [a.size for a in op.k] == [0]
     assert interpret(op, [torch.empty(20, 0), torch.empty(0, 24)]).abs().sum() == 0
+
+
+# ---- split-K planning (host only) -----------------------------------------------------
+
+
+def test_split_k_cuts_the_outermost_k_axis():
+    from torch_einshard._exec import _split_k
+    from torch_einshard.planner import ContractOp, SubAxis
+
+    # the einconv weight gradient of the benchmark: 256 x 2304 outputs over 16 x 64 x 64 positions
+    op = ContractOp((256, 2304), swapped=False, m=[SubAxis(256, a=1, c=2304)], n=[SubAxis(2304, b=1, c=1)],
+                    k=[SubAxis(16, a=1048576, b=1115136), SubAxis(64, a=16384, b=16896), SubAxis(64, a=256, b=256)])
+    split, parts = _split_k(op)
+    assert parts == 8
+    assert split.out_shape == (8, 256, 2304)
+    # the split axis runs first in the batch group and steps over whole parts
+    head = split.batch[0]
+    assert (head.size, head.a, head.b, head.c) == (8, 2 * 1048576, 2 * 1115136, 256 * 2304)
+    assert [(a.size, a.a, a.b) for a in split.k] == [(2, 1048576, 1115136), (64, 16384, 16896), (64, 256, 256)]
+
+
+def test_split_k_leaves_busy_or_short_contractions_alone():
+    from torch_einshard._exec import _split_k
+    from torch_einshard.planner import ContractOp, SubAxis
+
+    def op(m, n, k):
+        return ContractOp((m, n), swapped=False, m=[SubAxis(m, a=k, c=n)], n=[SubAxis(n, b=k, c=1)],
+                          k=[SubAxis(k, a=1, b=1)])
+
+    assert _split_k(op(4096, 4096, 65536))[1] == 1  # enough tiles already
+    assert _split_k(op(256, 256, 4096))[1] == 1     # K too short to pay
+    assert _split_k(op(64, 64, 8191))[1] == 1       # a prime K has no divisor to cut at
+    assert _split_k(op(64, 64, 16384))[1] == 32     # parts keep at least 512 of K
+
+
+def test_split_k_planned_contraction_checks_its_arithmetic():
+    # interpret the split op in fp64 on the CPU: partial sums over each part, then their sum
+    import torch
+
+    from torch_einshard._exec import _split_k
+    from torch_einshard.planner import ContractOp, SubAxis
+
+    m, n, k = 3, 5, 16384
+    x = torch.randn(k, m, dtype=torch.float64)
+    y = torch.randn(k, n, dtype=torch.float64)
+    op = ContractOp((m, n), swapped=False, m=[SubAxis(m, a=1, c=n)], n=[SubAxis(n, b=1, c=1)],
+                    k=[SubAxis(k, a=m, b=n)])
+    split, parts = _split_k(op)
+    head, rest = split.batch[0], split.k[0]
+    xf, yf = x.reshape(-1), y.reshape(-1)
+    partial = torch.zeros(parts, m, n, dtype=torch.float64)
+    for s in range(parts):
+        for r in range(rest.size):
+            ia = s * head.a + r * rest.a
+            ib = s * head.b + r * rest.b
+            partial[s] += torch.outer(xf[ia : ia + m], yf[ib : ib + n])
+    torch.testing.assert_close(partial.sum(0), x.T @ y)
