@@ -120,7 +120,8 @@ __device__ __forceinline__ OffT source_of(const GatherArgs& p, uint32_t v, bool&
     // the innermost dim counts vectors: its coordinate in elements is r << inner_shift
     coord[d] = d == R - 1 ? int32_t(r << p.inner_shift) : int32_t(r);
     if constexpr (M24) {
-      src += OffT(__umul24(r, uint32_t(p.out_stride[d])));
+      // dim 0 (never divided) may have a byte stride of 2^24 or more: a full multiply
+      src += d == 0 ? OffT(r) * OffT(p.out_stride[d]) : OffT(__umul24(r, uint32_t(p.out_stride[d])));
     } else {
       src += OffT(r) * OffT(p.out_stride[d]);
     }
@@ -1374,13 +1375,14 @@ extern "C" int es_gather(const es_gather_desc* d, const void* x, void* out, void
     if (reach > 0x3fffffffLL || p.base < -0x3fffffffLL || p.base > 0x3fffffffLL) off32 = false;
   }
   // 24-bit multiplies: fewer than 2^31 vectors, sizes and quotients below 2^23
-  // (v_mad_i32_i24 takes them signed), byte strides below 2^24
+  // (v_mad_i32_i24 takes them signed), byte strides below 2^24 (dim 0, which is never
+  // divided, takes a full multiply and any stride)
   Index index = off32 ? Index::k32 : Index::k64;
   if (off32 && total_vec < 0x80000000ull) {
     bool m24 = total_vec / p.out_div[rank - 1].d < (1u << 23);
     for (int i = 0; i < rank; ++i) {
       if (p.out_div[i].d >= (1u << 23)) m24 = false;
-      if (p.out_stride[i] >= (1 << 24)) m24 = false;
+      if (i > 0 && p.out_stride[i] >= (1 << 24)) m24 = false;  // dim 0: a full multiply
     }
     if (m24) index = Index::k24;
   }
