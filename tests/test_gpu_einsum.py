@@ -309,10 +309,12 @@ def test_repeated_calls_replay_with_fresh_data_and_geometry(gpu):
         # two K sub-axes (the inner one exactly one K tile), batch offsets
         ("m a k, n a k -> m n", [(4096, 3, 64), (4096, 3, 64)], "contract_pipe_256x256"),
         ("b m k, b n k -> b m n", [(16, 1024, 128), (16, 1000, 128)], "contract_pipe_256x256"),
-        # an M-contiguous operand: copied K-contiguous first, then the pipelined kernel
-        ("k m, n k -> m n", [(128, 4096), (4096, 128)], "contract_pipe_256x256"),
-        # both operands contiguous along M / N (the C2 pattern on both sides)
-        ("k m, k n -> m n", [(192, 4096), (192, 4136)], "contract_pipe_256x224"),
+        # operands contiguous along M / N: read in place, fragments through transposing
+        # LDS reads; ragged M and N edges
+        ("k m, n k -> m n", [(128, 4096), (4096, 128)], "contract_pipe_256x256_mn_a"),
+        ("m k, k n -> m n", [(4096, 128), (128, 4096)], "contract_pipe_256x256_mn_b"),
+        ("k m, k n -> m n", [(192, 4096), (192, 4136)], "contract_pipe_256x256_mn_ab"),
+        ("k m, n k -> m n", [(128, 4136), (4000, 128)], "contract_pipe_256x256_mn_a"),
     ],
 )
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -359,14 +361,55 @@ def test_output_rounding_is_bitexact(gpu, m, n, k, kernel):
     assert_bitexact_nan(got, want)
 
 
-def test_c2_pattern_repacks_one_operand(gpu):
-    # x is K-contiguous, y contiguous along its free axes: y alone is repacked
+def test_c2_pattern_reads_the_n_contiguous_operand_in_place(gpu):
+    # x is K-contiguous, y contiguous along its free axes; the planner makes y the
+    # first operand (so the output's contiguous axis a is along N), read M-contiguous
     x = randn(64, 32, 128, 64, seed=75, dtype=torch.bfloat16)
     y = randn(32, 64, 128, 16, seed=76, dtype=torch.bfloat16)
     expr = "a b k c, b c l d -> k l d a"
     got = es.einshard(expr, x.to(gpu), y.to(gpu))
-    assert _native.last_kernel() == "contract_pipe_256x256"
+    assert _native.last_kernel() == "contract_pipe_256x256_mn_a"
     assert_rel(got, einshard_cpu(expr, x, y), TOL[torch.bfloat16])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mn_contiguous_operand_with_two_k_levels(gpu, dtype):
+    # x sliced along its inner K axis: K stays two sub-axes (3 x 64), each K tile's 64
+    # k-rows one stride apart, the outer level a jump
+    big = randn(3, 80, 4096, seed=77, dtype=dtype)
+    x = big[:, :64, :]
+    y = randn(4096, 3, 64, seed=78, dtype=dtype)
+    expr = "k j m, n k j -> m n"
+    got = es.einshard(expr, x.to(gpu), y.to(gpu))
+    assert _native.last_kernel() == "contract_pipe_256x256_mn_a"
+    assert_rel(got, einshard_cpu(expr, x, y), TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mn_contiguous_rows_in_groups(gpu, dtype):
+    # x sliced along its unit-stride axis: M stays two sub-axes (200 x 24), so the
+    # 8-row runs of a 32-row block cross from one group of 24 rows to the next
+    x = randn(64, 200, 32, seed=79, dtype=dtype)[:, :, :24]
+    y = randn(64, 4104, seed=80, dtype=dtype)
+    expr = "k m a, k n -> m a n"
+    got = es.einshard(expr, x.to(gpu), y.to(gpu))
+    assert _native.last_kernel() == "contract_pipe_256x256_mn_ab"
+    assert_rel(got, einshard_cpu(expr, x, y), TOL[dtype])
+
+
+def test_mn_contiguous_output_rounding_is_bitexact(gpu):
+    # as test_output_rounding_is_bitexact, with both operands read along M / N
+    g = gen(92)
+    m, n, k = 4096, 4096, 64
+    xv, yv = torch.randn(m, generator=g) * 4, torch.randn(n, generator=g) * 4
+    xv[3], xv[5], yv[7] = float("inf"), float("nan"), -float("inf")
+    x = torch.zeros(k, m, dtype=torch.bfloat16)
+    y = torch.zeros(k, n, dtype=torch.bfloat16)
+    x[0], y[0] = xv.bfloat16(), yv.bfloat16()
+    got = es.einshard("k m, k n -> m n", x.to(gpu), y.to(gpu))
+    assert _native.last_kernel() == "contract_pipe_256x256_mn_ab"
+    want = (x[0].float()[:, None] * y[0].float()[None, :]).bfloat16()
+    assert_bitexact_nan(got, want)
 
 
 # ---- transposes (pure permutations whose input unit-stride dim is not innermost) ----

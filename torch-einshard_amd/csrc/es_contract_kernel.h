@@ -16,6 +16,8 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 // offset of linear index `i` of a group in the operand selected by WHICH
@@ -744,6 +746,92 @@ struct PipeCopies {
   }
 };
 
+// Copies of a tile whose operand is contiguous along its rows (M for A, N for B),
+// for contract_pipe.  The tile is stored as blocks of 32 rows: block b is 64 k-rows of
+// 64 bytes (rows 32b .. 32b + 31 of one k each), 4 KB, and 16-byte chunk c (8
+// consecutive rows) of k-row r sits at chunk position c ^ mn_swz(r).  One copy
+// instruction fills 16 k-rows of one block; lane l fetches k-row l / 4 of them, chunk
+// position l % 4.  Row runs past the edge re-read the last 8 rows (the host guarantees
+// that the row extent is a multiple of 8); they are never stored.
+__device__ __forceinline__ int mn_swz(int r) { return (((r >> 1) ^ (r >> 3)) & 1) << 1; }
+
+template <typename S, int ROWS, int NW, int SIDE>
+struct PipeCopiesMN {
+  static constexpr int NI = ROWS / 8 / NW;  // 1 KB copies of this wave per K tile
+  static_assert(NI >= 1 && ROWS % (8 * NW) == 0 && ROWS % 32 == 0, "tile shape");
+  uint32_t off[NI];
+  int region0;
+
+  __device__ __forceinline__ void init(const ContractArgs& p, int wave, int lane, uint32_t row0, int64_t boff) {
+    region0 = wave * NI;
+    const GroupArgs& g = SIDE == 0 ? p.gm : p.gn;
+    const uint32_t last = (SIDE == 0 ? p.M : p.N) - 8;
+    const int64_t kstride = SIDE == 0 ? p.ka_inner : p.kb_inner;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int q = region0 + i;
+      const int kr = (q % 4) * 16 + lane / 4;
+      const int chunk = (lane % 4) ^ mn_swz(kr);
+      uint32_t r = row0 + uint32_t((q / 4) * 32 + chunk * 8);
+      r = r > last ? last : r;
+      off[i] = uint32_t((boff + group_offset<SIDE>(g, r) + int64_t(kr) * kstride) * int64_t(sizeof(S)));
+    }
+  }
+  __device__ __forceinline__ void issue_one(int i, const void* base, uint32_t lds) const {
+    copy_to_lds(base, off[i], lds + uint32_t((region0 + i) * 1024));
+  }
+};
+
+// Fragment reads of contract_pipe: fragment i of a wave is 16 rows (its rows row0 + 16 i
+// onwards) by 8 k (k = 32 ks + 8 (lane / 16) .. +7 of the K tile), lane l holding row
+// l % 16: the operand layout of v_mfma_f32_16x16x32.  A K-contiguous tile gives each
+// lane its 16 bytes in one read.
+template <typename S, int LAYOUT>
+struct PipeFrag {
+  static constexpr int BK = kRowBytes / int(sizeof(S));
+  static constexpr int READS = 1;  // LDS read instructions per fragment
+  int ofs[2];                      // element offsets of substeps 0 and 1 in the side's tile
+
+  __device__ __forceinline__ void init(int lane, int row0) {
+    const int lrow = lane % 16;  // rows row0 + 16 i keep lrow's swizzle key
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) ofs[ks] = (row0 + lrow) * BK + swz(lrow, ks * 4 + lane / 16) * 8;
+  }
+  __device__ __forceinline__ uint4 read(const S* side, int i, int ks) const {
+    return *reinterpret_cast<const uint4*>(side + ofs[ks] + i * 16 * BK);
+  }
+};
+
+// An MN-contiguous tile (blocks of 32 rows, above) is read with gfx950's transposing
+// LDS read ds_read_b64_tr_b16.  Within each 16 lanes, lane j names 4 consecutive
+// 16-bit rows of k-row kb + j / 4 starting at row 4 (j % 4), and lane i receives
+// element i % 4 of lane 4e + i / 4's four as its element e: lane i then holds k-rows
+// kb .. kb + 3 of row i.  Two reads (kb and kb + 4) give one 8-deep fragment.  The 16
+// k-rows one read touches split evenly over the 32-byte slots of a 256-byte LDS line
+// through mn_swz: k-rows that share a slot pair ((r / 2) % 2 and r % 4 equal) differ
+// in (r / 8) % 2 and take opposite halves.
+template <typename S>
+struct PipeFrag<S, kMNContig> {
+  static constexpr int READS = 2;
+  int base[2];  // byte offsets in the side's tile of fragments with even / odd 16-row index
+
+  __device__ __forceinline__ void init(int lane, int row0) {  // row0: a multiple of 32
+    const int j = lane % 16, g = lane / 16, e = j / 4;
+    const int half = ((e >> 1) ^ g) & 1;  // mn_swz(8 g + e) / 2: also for k-rows + 4, + 32
+    const int b = (row0 / 32) * 4096 + (8 * g + e) * 64 + ((j % 4) >> 1) * 16 + (j & 1) * 8;
+    base[0] = b + 32 * half;
+    base[1] = b + 32 * (1 - half);
+  }
+  __device__ __forceinline__ uint4 read(const S* side, int i, int ks) const {
+    typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+    typedef __attribute__((address_space(3))) char lds_char;
+    const lds_char* p = (const lds_char*)side + base[i & 1] + (i >> 1) * 4096 + ks * 2048;
+    const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)p));
+    const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + 256)));
+    return make_uint4(lo[0], lo[1], hi[0], hi[1]);
+  }
+};
+
 // ---- software-pipelined kernel: 256 x BN tiles (BN = 256 or 224), 16-bit types -------
 // Four waves (2 x 2) each own 128 x BN/2 as 8 x BN/32 blocks of 16 x 16 on
 // v_mfma_f32_16x16x32_{bf16,f16}; a 64-deep K tile is two substeps of 32 k.  Two LDS
@@ -978,7 +1066,7 @@ __device__ __forceinline__ void store_pipe_t(const ContractArgs& p, typename Tra
   }
 }
 
-template <typename T, int BN, int L>
+template <typename T, int BN, int L, int LA, int LB>
 __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   using S = typename Traits<T>::S;
   constexpr int BM = 256, WM = 2, WN = 2;
@@ -989,12 +1077,16 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   constexpr int FM = WTM / 16, FN = WTN / 16;
   constexpr int STAGE = (BM + BN) * BK;
   constexpr int MMAS = FM * FN;  // per substep
-  using CopyA = PipeCopies<S, BM, WM * WN, 0>;
-  using CopyB = PipeCopies<S, BN, WM * WN, 1>;
+  using CopyA = std::conditional_t<LA == kMNContig, PipeCopiesMN<S, BM, WM * WN, 0>, PipeCopies<S, BM, WM * WN, 0>>;
+  using CopyB = std::conditional_t<LB == kMNContig, PipeCopiesMN<S, BN, WM * WN, 1>, PipeCopies<S, BN, WM * WN, 1>>;
+  using FragA = PipeFrag<S, LA>;
+  using FragB = PipeFrag<S, LB>;
+  constexpr int NREAD = FM * FragA::READS + FN * FragB::READS;  // LDS read instructions per substep
   constexpr int NCOPY = CopyA::NI + CopyB::NI;  // copies per wave per K tile
   static_assert(sizeof(S) == 2 && NS == 2, "16-bit element types, two substeps per K tile");
   static_assert(WTN % 16 == 0 && FM % 2 == 0, "tile shape");
-  static_assert(NCOPY <= MMAS && FM + FN <= MMAS, "last substep interleave");
+  static_assert(NCOPY <= MMAS && NREAD <= MMAS, "last substep interleave");
+  static_assert((LA == kKContig || WTM % 32 == 0) && (LB == kKContig || WTN % 32 == 0), "MN blocks of 32 rows");
 
   __shared__ __attribute__((aligned(1024))) S lds0[STAGE];
   __shared__ __attribute__((aligned(1024))) S lds1[STAGE];
@@ -1020,22 +1112,17 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
 
   f32x4 acc[FM][FN];  // first written by mma_first
 
-  // fragment rows of this lane are lane % 16 plus multiples of 16: one swizzle key
-  const int lrow = lane % 16;
-  int kofs[NS];
-#pragma unroll
-  for (int ks = 0; ks < NS; ++ks) kofs[ks] = lrow * BK + swz(lrow, ks * 4 + lane / 16) * VEC;
-  const int abase = wm * WTM * BK;
-  const int bbase = BM * BK + wn * WTN * BK;
+  FragA fa;
+  FragB fb;
+  fa.init(lane, wm * WTM);
+  fb.init(lane, wn * WTN);
 
   uint4 af[2][FM], bf[2][FN];
   auto frags = [&](const S* stage, int buf, int ks) {
-    const S* a = stage + abase + kofs[ks];
-    const S* b = stage + bbase + kofs[ks];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const uint4*>(a + i * 16 * BK);
+    for (int i = 0; i < FM; ++i) af[buf][i] = fa.read(stage, i, ks);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) bf[buf][j] = *reinterpret_cast<const uint4*>(b + j * 16 * BK);
+    for (int j = 0; j < FN; ++j) bf[buf][j] = fb.read(stage + BM * BK, j, ks);
   };
 
   const uint32_t nk = (p.K + BK - 1) / BK;  // >= 1: an empty K takes the generic kernel
@@ -1072,7 +1159,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
     for (int q = 0; q < MMAS; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
       // the fragment reads spread evenly over the substep
-      if ((q * (FM + FN)) / MMAS != ((q + 1) * (FM + FN)) / MMAS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if ((q * NREAD) / MMAS != ((q + 1) * NREAD) / MMAS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     // K tile kt+1 complete for everyone; every read of stage kt done
@@ -1088,8 +1175,8 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
       if (c0 != c1) copy(c0, cur_addr);
       const int r0 = (q * (FM + FN)) / MMAS, r1 = ((q + 1) * (FM + FN)) / MMAS;
       if (r0 != r1) {
-        if (r0 < FM) af[0][r0] = *reinterpret_cast<const uint4*>(stage_nxt + abase + kofs[0] + r0 * 16 * BK);
-        else bf[0][r0 - FM] = *reinterpret_cast<const uint4*>(stage_nxt + bbase + kofs[0] + (r0 - FM) * 16 * BK);
+        if (r0 < FM) af[0][r0] = fa.read(stage_nxt, r0, 0);
+        else bf[0][r0 - FM] = fb.read(stage_nxt + BM * BK, r0 - FM, 0);
       }
     }
     w.advance(nk);
@@ -1118,12 +1205,12 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
 
 // ---- launcher ----------------------------------------------------------------------
 // contract_pipe keeps as many K walk levels as the descriptor has (1, 2, or up to 4)
-template <typename T, int BN>
+template <typename T, int BN, int LA, int LB>
 void launch_pipe(const ContractArgs& p, hipStream_t s) {
   switch (p.klevels) {
-    case 1: contract_pipe<T, BN, 1><<<p.total_tiles, 256, 0, s>>>(p); break;
-    case 2: contract_pipe<T, BN, 2><<<p.total_tiles, 256, 0, s>>>(p); break;
-    default: contract_pipe<T, BN, kKLevels><<<p.total_tiles, 256, 0, s>>>(p); break;
+    case 1: contract_pipe<T, BN, 1, LA, LB><<<p.total_tiles, 256, 0, s>>>(p); break;
+    case 2: contract_pipe<T, BN, 2, LA, LB><<<p.total_tiles, 256, 0, s>>>(p); break;
+    default: contract_pipe<T, BN, kKLevels, LA, LB><<<p.total_tiles, 256, 0, s>>>(p); break;
   }
 }
 
@@ -1136,20 +1223,32 @@ int launch_one(const ContractArgs& p, hipStream_t s, const char* name) {
 
 template <typename T, int BM, int BN, int WM, int WN, int PF>
 int launch_layouts(const ContractArgs& p, int la, int lb, hipStream_t s, const char* name) {
-  if (la == kKContig && lb == kKContig) {
-    if constexpr (BM == 256 && BN == 256 && sizeof(typename Traits<T>::S) == 2) {
-      if (!p.off32) return launch_one<T, BM, BN, WM, WN, kKContig, kKContig, PF>(p, s, name);
-      if (p.pipe_bn == 224) {
-        launch_pipe<T, 224>(p, s);
-        set_kernel("contract_pipe_256x224");
+  if constexpr (BM == 256 && BN == 256 && sizeof(typename Traits<T>::S) == 2) {
+    // contract_pipe when every offset fits 32 bits; an MN-contiguous operand is read
+    // through transposing LDS reads (256-wide tiles only)
+    if (p.off32) {
+      if (la == kKContig && lb == kKContig) {
+        if (p.pipe_bn == 224) {
+          launch_pipe<T, 224, kKContig, kKContig>(p, s);
+          set_kernel("contract_pipe_256x224");
+        } else {
+          launch_pipe<T, 256, kKContig, kKContig>(p, s);
+          set_kernel("contract_pipe_256x256");
+        }
+      } else if (la == kKContig && lb == kMNContig) {
+        launch_pipe<T, 256, kKContig, kMNContig>(p, s);
+        set_kernel("contract_pipe_256x256_mn_b");
+      } else if (la == kMNContig && lb == kKContig) {
+        launch_pipe<T, 256, kMNContig, kKContig>(p, s);
+        set_kernel("contract_pipe_256x256_mn_a");
       } else {
-        launch_pipe<T, 256>(p, s);
-        set_kernel("contract_pipe_256x256");
+        launch_pipe<T, 256, kMNContig, kMNContig>(p, s);
+        set_kernel("contract_pipe_256x256_mn_ab");
       }
       return check_launch("es_contract");
     }
-    return launch_one<T, BM, BN, WM, WN, kKContig, kKContig, PF>(p, s, name);
   }
+  if (la == kKContig && lb == kKContig) return launch_one<T, BM, BN, WM, WN, kKContig, kKContig, PF>(p, s, name);
   if (la == kKContig && lb == kMNContig) return launch_one<T, BM, BN, WM, WN, kKContig, kMNContig, PF>(p, s, name);
   if (la == kMNContig && lb == kKContig) return launch_one<T, BM, BN, WM, WN, kMNContig, kKContig, PF>(p, s, name);
   if (la == kMNContig && lb == kMNContig) return launch_one<T, BM, BN, WM, WN, kMNContig, kMNContig, 1>(p, s, name);

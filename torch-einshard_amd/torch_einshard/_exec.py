@@ -158,11 +158,13 @@ def run_gather(desc, x, out):
     call("es_gather", ctypes.byref(desc), _ptr(x), _ptr(out), _native.stream_of(out))
 
 
-# The 256 x 256 contraction kernel for 16-bit types needs both operands K-contiguous
-# (innermost K sub-axis of unit stride, a whole number of 64-deep K tiles).  When it
-# would be chosen (enough tiles for every CU) and an operand is instead contiguous
-# along M or N, that operand is first copied K-contiguous into a temporary: one
-# es_gather over its bytes buys the faster kernel.
+# The 256 x 256 contraction kernel for 16-bit types (contract_pipe) reads each operand
+# K-contiguous (innermost K sub-axis of unit stride, a whole number of 64-deep K
+# tiles) or contiguous along its rows (M for x, N for y: innermost row sub-axis of unit
+# stride, 8-element runs, every other stride a multiple of 8), with every byte offset
+# below 2^32.  When it would be chosen (enough tiles for every CU) and an operand fits
+# neither while its rows are still the unit-stride axis, that operand is first copied
+# K-contiguous into a temporary: one es_gather over its bytes buys the faster kernel.
 _BIG_TILE = 256
 _CU_TILES = 256
 _K_TILE_BYTES = 128
@@ -175,6 +177,21 @@ def _prod(values):
     return out
 
 
+def _max_offset_bytes(op, field, rows, elem_size):
+    axes = list(op.batch) + list(rows) + list(op.k)
+    return sum((a.size - 1) * abs(getattr(a, field)) for a in axes if a.size > 0) * elem_size
+
+
+def _rows_contiguous_ok(op, field, rows, elem_size):
+    """contract_pipe's test for an operand contiguous along its rows (its other
+    conditions, K tiles and 32-bit offsets, are checked by the caller)."""
+    vec = 16 // elem_size
+    if getattr(rows[-1], field) != 1 or rows[-1].size % vec:
+        return False
+    others = list(op.batch) + list(rows[:-1]) + list(op.k)
+    return all(getattr(a, field) % vec == 0 for a in others)
+
+
 def _repack_for_k_contiguity(op, order, elem_size):
     if elem_size != 2 or not op.k or not op.m or not op.n:
         return op, ()
@@ -183,12 +200,15 @@ def _repack_for_k_contiguity(op, order, elem_size):
     if tiles < _CU_TILES:
         return op, ()
     k_tile = _K_TILE_BYTES // elem_size
+    off32 = all(_max_offset_bytes(op, f, r, elem_size) + 16 < 1 << 32 for f, r in (("a", op.m), ("b", op.n)))
     repack = []
     for field, rows, index in (("a", op.m, order[0]), ("b", op.n, order[1])):
         k_ok = getattr(op.k[-1], field) == 1 and op.k[-1].size % k_tile == 0
         rows_inner = getattr(rows[-1], field) == 1
         if k_ok or not rows_inner:
             continue
+        if off32 and op.k[-1].size % k_tile == 0 and _rows_contiguous_ok(op, field, rows, elem_size):
+            continue  # read in place through transposing LDS reads
         axes = list(op.batch) + list(rows) + list(op.k)
         if len(axes) > MAX_AXES:
             continue
