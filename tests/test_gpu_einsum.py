@@ -493,3 +493,28 @@ def test_split_k(gpu, m, n, k, dtype):
     assert _native.last_kernel().startswith("reduce"), _native.last_kernel()
     want = einshard_cpu("k m, k n -> m n", x.float(), y.float())
     assert_rel(got, want.to(dtype), TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_split_k_on_the_pipelined_kernel(gpu, dtype):
+    # a weight gradient with 4 x 8 tiles of 256 x 256 and K = 8192: eight parts of 1024
+    # make 256 tiles for the pipelined kernel, both operands read along their rows
+    from torch_einshard import _cache
+
+    x = randn(8, 1024, 1024, seed=97, dtype=dtype)
+    y = randn(8, 1024, 2048, seed=98, dtype=dtype)
+    expr = "b n h, b n c -> h c"
+    xs = [x.to(gpu), y.to(gpu)]
+    got = es.einshard(expr, *xs)
+    assert_rel(got, einshard_cpu(expr, x.float(), y.float()).to(dtype), TOL[dtype])
+    prep, _ = _cache.lookup(_cache.call_key("einshard", xs, None, None, expr, None, None))
+    parts = prep.split[0]
+    assert parts == 8
+    # the partial contractions alone: their kernel, and each part's sum
+    tmp = torch.empty((parts, 1024 * 2048), dtype=dtype, device=gpu)
+    ptrs = [xs[i].data_ptr() for i in prep.order]
+    assert _native.lib().es_contract(prep.ref, *ptrs, tmp.data_ptr(), _native.stream_of(tmp)) == 0
+    assert _native.last_kernel() == "contract_pipe_256x256_mn_ab"
+    for s in (0, parts - 1):
+        want = einshard_cpu(expr, x[s:s + 1].float(), y[s:s + 1].float())
+        assert_rel(tmp[s].view(1024, 2048), want.to(dtype), TOL[dtype])

@@ -258,3 +258,30 @@ def test_split_k_planned_contraction_checks_its_arithmetic():
             ib = s * head.b + r * rest.b
             partial[s] += torch.outer(xf[ia : ia + m], yf[ib : ib + n])
     torch.testing.assert_close(partial.sum(0), x.T @ y)
+
+
+def test_split_k_targets_the_pipelined_kernel_for_16_bit_weight_gradients():
+    from torch_einshard._exec import _split_k
+    from torch_einshard.planner import ContractOp, SubAxis
+
+    # config 4's weight gradient (b n h, b n c -> h c): 7 x 16 tiles of 256 x 256 over
+    # K = 16384, both operands contiguous along their rows.  Four parts make 448 tiles
+    # for the pipelined kernel; without the element size only the 128 x 128 rule runs.
+    def wgrad(m, n, k, k_inner_a=None):
+        return ContractOp((m, n), swapped=False, m=[SubAxis(m, a=1, c=n)], n=[SubAxis(n, b=1, c=1)],
+                          k=[SubAxis(k, a=k_inner_a or m, b=n)])
+
+    split, parts = _split_k(wgrad(1792, 4096, 16384), 2)
+    assert parts == 4
+    assert [(a.size, a.a, a.b) for a in split.k] == [(4096, 1792, 4096)]
+    head = split.batch[0]
+    assert (head.size, head.a, head.b, head.c) == (4, 4096 * 1792, 4096 * 4096, 1792 * 4096)
+    assert _split_k(wgrad(1792, 4096, 16384))[1] == 1
+    # parts of at least 1024 of K, and enough tiles that every CU has one
+    assert _split_k(wgrad(1024, 2048, 8192), 2)[1] == 8
+    assert _split_k(wgrad(1024, 2048, 4096), 2)[1] == 1  # K shorter than the split minimum
+    # operands the pipelined kernel cannot read in place keep the 128 x 128 rule:
+    # row strides that are not a multiple of 8 elements
+    assert _split_k(wgrad(1792, 4096, 16384, k_inner_a=1793), 2)[1] == 1
+    # a whole number of 64-deep K tiles is required
+    assert _split_k(wgrad(1792, 4096, 16383), 2)[1] == 1

@@ -251,21 +251,78 @@ _SPLIT_TARGET = 256     # aim for this many tiles
 _SPLIT_K_PART = 512     # and keep at least this much K in each part
 
 
-def _split_k(op):
-    """(op with a leading split batch axis, partial count) or (op, 1)."""
+# A 16-bit contraction that contract_pipe can read (both operands K-contiguous or
+# contiguous along their rows, 32-bit offsets) but that has fewer than one 256 x 256
+# tile per CU runs on 128 x 128 tiles at about half the speed per flop.  It is split
+# instead into parts that give the pipelined kernel at least a tile per CU when a
+# cycle model says so: per round of tiles, K steps times the cost of one plus a fixed
+# prologue and epilogue, and the reduction's bytes.  The constants are measured
+# (MI355X, ~2 GHz under MFMA load): a 64-deep K step of a 256 x 256 pipelined tile
+# 2,450 cycles, its prologue and epilogue 23,300; a 128 x 128 tile's step 1,750
+# cycles (448 us for the 1792 x 4096 x 16384 weight gradient); es_reduce ~2,500 bytes
+# per cycle.
+_PIPE_STEP = 2450
+_PIPE_FIXED = 23300
+_T128_STEP = 1750
+_T128_FIXED = 6000
+_REDUCE_BYTES_PER_CYCLE = 2500
+_PIPE_K_PART = 1024     # K per part of a pipelined split: 16 K steps
+
+
+def _pipe_readable(op, elem_size):
+    """The host conditions of contract_pipe for both operands (es_contract.hip: a
+    whole number of 64-deep K tiles, each operand K-contiguous or contiguous along its
+    rows, at most 4 K sub-axes, every byte offset below 2^32)."""
+    k_tile = _K_TILE_BYTES // elem_size
+    vec = 16 // elem_size
+    if elem_size != 2 or not op.k or len(op.k) > 4 or op.k[-1].size % k_tile:
+        return False
+    for field, rows in (("a", op.m), ("b", op.n)):
+        if _max_offset_bytes(op, field, rows, elem_size) + 16 >= 1 << 32:
+            return False
+        k_contig = getattr(op.k[-1], field) == 1 and all(
+            getattr(a, field) % vec == 0 for a in list(op.batch) + list(rows) + list(op.k[:-1]))
+        if not k_contig and not _rows_contiguous_ok(op, field, rows, elem_size):
+            return False
+    return True
+
+
+def _rounds(tiles):
+    return -(-tiles // _CU_TILES)
+
+
+def _split_k(op, elem_size=None):
+    """(op with a leading split batch axis, partial count) or (op, 1).  ``elem_size``
+    2 lets a split target the pipelined kernel."""
     if not op.k or not op.m or not op.n:
         return op, 1
-    tiles = _prod(a.size for a in op.batch)
-    tiles *= -(-_prod(a.size for a in op.m) // _SPLIT_TILE) * -(-_prod(a.size for a in op.n) // _SPLIT_TILE)
+    nb = _prod(a.size for a in op.batch)
+    m, n = _prod(a.size for a in op.m), _prod(a.size for a in op.n)
+    tiles = nb * -(-m // _SPLIT_TILE) * -(-n // _SPLIT_TILE)
     k_total = _prod(a.size for a in op.k)
-    if tiles >= _SPLIT_BELOW or k_total < _SPLIT_MIN_K:
+    if k_total < _SPLIT_MIN_K:
         return op, 1
     outer = op.k[0]
-    want = -(-_SPLIT_TARGET // tiles)
+    divisors = [d for d in range(2, outer.size + 1) if outer.size % d == 0]
     best = 1
-    for d in range(2, outer.size + 1):
-        if outer.size % d == 0 and d <= want and k_total // d >= _SPLIT_K_PART:
-            best = d
+    if tiles < _SPLIT_BELOW:
+        want = -(-_SPLIT_TARGET // tiles)
+        for d in divisors:
+            if d <= want and k_total // d >= _SPLIT_K_PART:
+                best = d
+    tiles256 = nb * -(-m // _BIG_TILE) * -(-n // _BIG_TILE)
+    if elem_size == 2 and tiles256 < _CU_TILES and _pipe_readable(op, elem_size):
+        out_bytes = _prod(op.out_shape) * elem_size
+        cost = _rounds(tiles * best) * (k_total // best // 64 * _T128_STEP + _T128_FIXED)
+        if best > 1:
+            cost += (best + 1) * out_bytes / _REDUCE_BYTES_PER_CYCLE
+        for d in divisors:
+            if tiles256 * d < _CU_TILES or k_total // d < _PIPE_K_PART:
+                continue
+            c = _rounds(tiles256 * d) * (k_total // d // 64 * _PIPE_STEP + _PIPE_FIXED)
+            c += (d + 1) * out_bytes / _REDUCE_BYTES_PER_CYCLE
+            if c < cost:
+                cost, best = c, d
     if best == 1:
         return op, 1
     out_numel = _prod(op.out_shape)
@@ -331,7 +388,7 @@ def prepare_op(op, dtype, elem_size, split=True):
         out_shape = op.out_shape
         parts = 1
         if split:
-            op, parts = _split_k(op)
+            op, parts = _split_k(op, elem_size)
         desc = ContractDesc()
         desc.dtype = code
         desc.n_batch = _set_axes(desc.batch, op.batch, "einshard")
