@@ -285,3 +285,33 @@ def test_split_k_targets_the_pipelined_kernel_for_16_bit_weight_gradients():
     assert _split_k(wgrad(1792, 4096, 16384, k_inner_a=1793), 2)[1] == 1
     # a whole number of 64-deep K tiles is required
     assert _split_k(wgrad(1792, 4096, 16383), 2)[1] == 1
+
+
+def test_split_k_cut_through_two_k_axes_checks_its_arithmetic(monkeypatch):
+    # A short outer K sub-axis is cut whole and the next one in parts (an einconv
+    # weight gradient: 16 batch rows of positions).  Thresholds are lowered so that a
+    # small case takes this cut; the split op is interpreted in fp64 from its
+    # descriptors, and its partials must sum to the contraction.
+    from torch_einshard import _exec
+
+    monkeypatch.setattr(_exec, "_CU_TILES", 16)
+    monkeypatch.setattr(_exec, "_PIPE_K_PART", 64)
+    monkeypatch.setattr(_exec, "_PIPE_FIXED", 0)
+    monkeypatch.setattr(_exec, "_SPLIT_MIN_K", 1024)
+    b, h, w, o, t = 2, 16, 64, 256, 512
+    gz = torch.randn(b, h, w + 8, o, dtype=torch.float64)[:, :, :w]  # K sub-axes that do not merge
+    xp = torch.randn(b, h + 2, w, t, dtype=torch.float64)[:, :h]
+    op = lower_einsum([list("bhwo"), list("bhwt")], [tuple(gz.shape), tuple(xp.shape)],
+                      [gz.stride(), xp.stride()], list("ot"))
+    assert [a.size for a in op.k] == [2, 16, 64]
+    split, parts = _exec._split_k(op, 2)
+    assert parts == 8  # 2 whole outer rows x 4 runs of the second sub-axis
+    assert [a.size for a in split.batch] == [2, 4] and [a.size for a in split.k] == [4, 64]
+    partial = interpret(split, [gz, xp])
+    assert partial.shape == (8, o, t)
+    torch.testing.assert_close(partial.sum(0), torch.einsum("bhwo,bhwt->ot", gz, xp))
+    # every part covers a distinct quarter of one outer row
+    for p in range(parts):
+        i, j = divmod(p, 4)
+        want = torch.einsum("hwo,hwt->ot", gz[i, 4 * j:4 * j + 4], xp[i, 4 * j:4 * j + 4])
+        torch.testing.assert_close(partial[p], want)

@@ -246,15 +246,27 @@ __global__ __launch_bounds__(kThreads) void reduce_rows(const ReduceArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// second pass: out[o] = sum_s partial[s][o], s in increasing order
+// second pass: out[o] = sum_s partial[s][o], s in increasing order.  A narrow output
+// (a bias gradient: a few hundred columns over thousands of partials) leaves one
+// work-group, so each thread loads 16 partials ahead of adding them in order: the
+// loads overlap, the sum stays sequential.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void reduce_finish(const float* partial, void* out, uint32_t n_out,
                                                           uint32_t nsplit) {
   using S = typename Elem<T>::storage;
+  constexpr uint32_t kAhead = 16;
   const uint32_t o = blockIdx.x * kThreads + threadIdx.x;
   if (o >= n_out) return;
   float acc = 0.f;
-  for (uint32_t s = 0; s < nsplit; ++s) acc += partial[size_t(s) * n_out + o];
+  uint32_t s = 0;
+  for (; s + kAhead <= nsplit; s += kAhead) {
+    float v[kAhead];
+#pragma unroll
+    for (uint32_t u = 0; u < kAhead; ++u) v[u] = partial[size_t(s + u) * n_out + o];
+#pragma unroll
+    for (uint32_t u = 0; u < kAhead; ++u) acc += v[u];
+  }
+  for (; s < nsplit; ++s) acc += partial[size_t(s) * n_out + o];
   static_cast<S*>(out)[o] = Elem<T>::store(acc);
 }
 

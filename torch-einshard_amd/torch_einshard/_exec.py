@@ -310,26 +310,41 @@ def _split_k(op, elem_size=None):
         for d in divisors:
             if d <= want and k_total // d >= _SPLIT_K_PART:
                 best = d
+    inner = 1  # > 1: the outer K sub-axis is cut whole and the next one into `inner` parts
     tiles256 = nb * -(-m // _BIG_TILE) * -(-n // _BIG_TILE)
     if elem_size == 2 and tiles256 < _CU_TILES and _pipe_readable(op, elem_size):
         out_bytes = _prod(op.out_shape) * elem_size
         cost = _rounds(tiles * best) * (k_total // best // 64 * _T128_STEP + _T128_FIXED)
         if best > 1:
             cost += (best + 1) * out_bytes / _REDUCE_BYTES_PER_CYCLE
-        for d in divisors:
+        # a short outer sub-axis (a batch of 16 positions' rows) also cuts into the next
+        cuts = [(d, 1) for d in divisors]
+        if len(op.k) > 2:
+            second = op.k[1].size
+            cuts += [(outer.size * d, d) for d in range(2, second + 1) if second % d == 0]
+        for d, d2 in cuts:
             if tiles256 * d < _CU_TILES or k_total // d < _PIPE_K_PART:
                 continue
             c = _rounds(tiles256 * d) * (k_total // d // 64 * _PIPE_STEP + _PIPE_FIXED)
             c += (d + 1) * out_bytes / _REDUCE_BYTES_PER_CYCLE
             if c < cost:
-                cost, best = c, d
+                cost, best, inner = c, d, d2
     if best == 1:
         return op, 1
     out_numel = _prod(op.out_shape)
+    out_shape = (best,) + tuple(op.out_shape)
+    if inner > 1:
+        # part p = i * inner + j: all of outer position i, the j-th run of the next sub-axis
+        second = op.k[1]
+        rest = second.size // inner
+        split = [SubAxis(outer.size, a=outer.a, b=outer.b, c=inner * out_numel, label="split"),
+                 SubAxis(inner, a=second.a * rest, b=second.b * rest, c=out_numel, label="split")]
+        k = ([SubAxis(rest, a=second.a, b=second.b, label=second.label)] if rest > 1 else []) + list(op.k[2:])
+        return replace(op, out_shape=out_shape, batch=split + list(op.batch), k=k), best
     rest = outer.size // best
     split_axis = SubAxis(best, a=outer.a * rest, b=outer.b * rest, c=out_numel, label="split")
     k = ([SubAxis(rest, a=outer.a, b=outer.b, label=outer.label)] if rest > 1 else []) + list(op.k[1:])
-    return replace(op, out_shape=(best,) + tuple(op.out_shape), batch=[split_axis] + list(op.batch), k=k), best
+    return replace(op, out_shape=out_shape, batch=[split_axis] + list(op.batch), k=k), best
 
 
 def prepare_op(op, dtype, elem_size, split=True):
