@@ -283,8 +283,9 @@ def test_split_k_targets_the_pipelined_kernel_for_16_bit_weight_gradients():
     # operands the pipelined kernel cannot read in place keep the 128 x 128 rule:
     # row strides that are not a multiple of 8 elements
     assert _split_k(wgrad(1792, 4096, 16384, k_inner_a=1793), 2)[1] == 1
-    # a whole number of 64-deep K tiles is required
+    # a whole number of 64-deep K tiles is required, in the whole K and in each part
     assert _split_k(wgrad(1792, 4096, 16383), 2)[1] == 1
+    assert _split_k(wgrad(1792, 4096, 64 * 257), 2)[1] == 1  # 257 tiles: no whole-tile cut
 
 
 def test_split_k_cut_through_two_k_axes_checks_its_arithmetic(monkeypatch):

@@ -325,6 +325,8 @@ def _split_k(op, elem_size=None):
         for d, d2 in cuts:
             if tiles256 * d < _CU_TILES or k_total // d < _PIPE_K_PART:
                 continue
+            if len(op.k) == 1 and (outer.size // d) % (_K_TILE_BYTES // elem_size):
+                continue  # a cut through the innermost K sub-axis keeps whole K tiles
             c = _rounds(tiles256 * d) * (k_total // d // 64 * _PIPE_STEP + _PIPE_FIXED)
             c += (d + 1) * out_bytes / _REDUCE_BYTES_PER_CYCLE
             if c < cost:
