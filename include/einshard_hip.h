@@ -131,7 +131,8 @@ int es_reduce(const es_reduce_desc* desc, const void* x, const void* y, void* ou
  * with every group given as sub-axes (outermost first).  Strides: A uses .a of
  * batch/m/k, B uses .b of batch/n/k, C uses .c of batch/m/n (explicit output
  * strides).  An empty group has extent 1.  bf16/f16 run on
- * v_mfma_f32_16x16x32_{bf16,f16} (large problems with K-contiguous operands) or
+ * v_mfma_f32_16x16x32_{bf16,f16} (large problems; an operand contiguous along M or
+ * N is transposed in the LDS read, ds_read_b64_tr_b16) or
  * v_mfma_f32_32x32x16_{bf16,f16}, f32 on v_mfma_f32_32x32x2_f32; fp32
  * accumulation, one rounding of the result.  Operand layouts are read in place
  * (no transposed copy): either the innermost K sub-axis or the innermost M
