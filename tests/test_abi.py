@@ -52,6 +52,30 @@ def test_library_loads_and_reports_version():
         assert hasattr(lib, name)
 
 
+def _integration_stub_classes():
+    """The ctypes classes of INTEGRATION.md's binding example, executed without the
+    library (the CDLL line and everything after the classes are left out)."""
+    doc = os.path.join(os.path.dirname(HEADER), os.pardir, "INTEGRATION.md")
+    text = open(doc).read()
+    block = next(b for b in re.findall(r"```python\n(.*?)```", text, flags=re.S) if "class es_axis" in b)
+    start = block.index("class es_axis")
+    end = block.index("_lib.es_contract.argtypes")
+    scope = {"ctypes": ctypes}
+    exec(block[start:end], scope)
+    return scope["es_axis"], scope["es_contract_desc"]
+
+
+def test_integration_stub_matches_the_abi_field_for_field():
+    stub_axis, stub_desc = _integration_stub_classes()
+    for stub, mirror in ((stub_axis, _native.EsAxis), (stub_desc, _native.ContractDesc)):
+        assert ctypes.sizeof(stub) == ctypes.sizeof(mirror), stub.__name__
+        names = [f[0] for f in stub._fields_]
+        assert names == [f[0] for f in mirror._fields_], stub.__name__
+        for name in names:
+            a, b = getattr(stub, name), getattr(mirror, name)
+            assert (a.offset, a.size) == (b.offset, b.size), (stub.__name__, name)
+
+
 def test_descriptor_layouts_match_the_header():
     # sizes of the ctypes mirrors equal the C structs (int64 fields, 8 axes per group)
     assert ctypes.sizeof(_native.EsAxis) == 32

@@ -65,6 +65,12 @@ struct ContractArgs {
   uint32_t tiles_m, tiles_n;
   uint32_t group_n;      // N-tiles per tile group (divides tiles_n; see tile_of)
   uint32_t total_tiles;
+  FastDiv tdiv_batch;    // divides by the tiles of one batch entry (tiles_m * tiles_n)
+  FastDiv tdiv_group;    // ... of one tile group (tiles_m * group_n)
+  FastDiv tdiv_gn;       // ... by group_n
+  // the largest sub-axis count of gb, gm and gn when it is at most 2 (at least 1), else 0:
+  // contract_pipe's bounded-group instantiations unroll the offset walks to that many
+  int32_t gdims;
   uint32_t pipe_bn;      // 224: contract_pipe's 256 x 224 tiles; 0: 256 x 256
   int32_t vstore;        // 16-byte vector stores: 1 along n; 2 along m (contract_pipe only)
   int32_t off32;         // every byte offset into A and B fits in 32 bits

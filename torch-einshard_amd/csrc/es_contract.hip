@@ -325,6 +325,13 @@ int contract(const es_contract_desc* d, const void* a, const void* b, const void
   p.tiles_n = uint32_t(tn);
   p.total_tiles = uint32_t(total);
   p.group_n = group_width(tm, tn, total);
+  p.tdiv_batch.init(uint32_t(tm * tn));
+  p.tdiv_group.init(uint32_t(tm * p.group_n));
+  p.tdiv_gn.init(p.group_n);
+  {
+    const int most = std::max(d->n_batch, std::max(d->n_m, d->n_n));
+    p.gdims = most <= 2 ? std::max(most, 1) : 0;
+  }
   p.halo_n = 0;
   if (halo != nullptr && (st = halo_args(d, halo, esz, la, lb, config, bk, p)) != ES_OK) return st;
 

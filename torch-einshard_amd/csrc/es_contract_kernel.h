@@ -189,16 +189,51 @@ struct KWalk {
 // logical tiles; logical tiles walk groups of group_n N-tiles, M fastest inside a
 // group, so that run is a compact rectangle of group_n N-tiles by run / group_n
 // M-tiles and the XCD's L2 sees few distinct A and B panels.
+// The three divisions use divisors prepared on the host (a multiply-high and a shift
+// each instead of an integer division sequence).
 __device__ __forceinline__ void tile_of(const ContractArgs& p, uint32_t b, uint32_t& bidx, uint32_t& tm, uint32_t& tn) {
   if (p.total_tiles % 8 == 0) b = (b % 8) * (p.total_tiles / 8) + b / 8;
-  const uint32_t per_batch = p.tiles_m * p.tiles_n;
-  bidx = b / per_batch;
-  const uint32_t rem = b - bidx * per_batch;
-  const uint32_t gsize = p.tiles_m * p.group_n;  // tiles per group
-  const uint32_t g = rem / gsize;
-  const uint32_t r = rem - g * gsize;
-  tm = r / p.group_n;
+  bidx = p.tdiv_batch.div31(b);
+  const uint32_t rem = b - bidx * p.tdiv_batch.d;
+  const uint32_t g = p.tdiv_group.div31(rem);
+  const uint32_t r = rem - g * p.tdiv_group.d;
+  tm = p.tdiv_gn.div31(r);
   tn = g * p.group_n + (r - tm * p.group_n);
+}
+
+// Offset of index i of a group in the operand selected by WHICH: the generic walk over
+// the sub-axes (G = 0), or (G > 0: the group has at most G sub-axes; the unused ones have
+// extent 1 and stride 0) G - 1 divisions, unrolled, with the outermost sub-axis taking
+// the quotient left (i is below the group's extent).
+template <int WHICH, int G>
+__device__ __forceinline__ int64_t group_offset_d(const GroupArgs& g, uint32_t i) {
+  if constexpr (G == 0) {
+    return group_offset<WHICH>(g, i);
+  } else {
+    int64_t off = 0;
+#pragma unroll
+    for (int d = G - 1; d > 0; --d) {
+      uint32_t r;
+      i = g.div[d].divmod(i, r);
+      off += int64_t(r) * (WHICH == 0 ? g.sa[d] : (WHICH == 1 ? g.sb[d] : g.sc[d]));
+    }
+    return off + int64_t(i) * (WHICH == 0 ? g.sa[0] : (WHICH == 1 ? g.sb[0] : g.sc[0]));
+  }
+}
+
+// The same in 32 bits (a row's offset within an operand whose every offset fits 32 bits;
+// `scale` the element size): the low 32 bits of group_offset_d's result times scale.
+template <int WHICH, int G>
+__device__ __forceinline__ uint32_t group_offset_d32(const GroupArgs& g, uint32_t i, uint32_t scale) {
+  static_assert(G > 0, "bounded groups only");
+  uint32_t off = 0;
+#pragma unroll
+  for (int d = G - 1; d > 0; --d) {
+    uint32_t r;
+    i = g.div[d].divmod(i, r);
+    off += r * uint32_t((WHICH == 0 ? g.sa[d] : (WHICH == 1 ? g.sb[d] : g.sc[d])) * scale);
+  }
+  return off + i * uint32_t((WHICH == 0 ? g.sa[0] : (WHICH == 1 ? g.sb[0] : g.sc[0])) * scale);
 }
 
 // ---- tile loaders -------------------------------------------------------------
@@ -433,6 +468,27 @@ __device__ __forceinline__ int64_t group_offset_k(KGroup g, uint32_t i) {
     off += int64_t(r) * (WHICH == 0 ? g->sa[d] : (WHICH == 1 ? g->sb[d] : g->sc[d]));
   }
   return off;
+}
+
+// group_offset_k, or (G > 0) group_offset_d's bounded walk, unrolled
+template <int WHICH, int G>
+__device__ __forceinline__ int64_t group_offset_kd(KGroup g, uint32_t i) {
+  if constexpr (G == 0) {
+    return group_offset_k<WHICH>(g, i);
+  } else {
+    int64_t off = 0;
+#pragma unroll
+    for (int d = G - 1; d > 0; --d) {
+      FastDiv f;
+      f.d = g->div[d].d;
+      f.m = g->div[d].m;
+      f.l = g->div[d].l;
+      uint32_t r;
+      i = f.divmod(i, r);
+      off += int64_t(r) * (WHICH == 0 ? g->sa[d] : (WHICH == 1 ? g->sb[d] : g->sc[d]));
+    }
+    return off + int64_t(i) * (WHICH == 0 ? g->sa[0] : (WHICH == 1 ? g->sb[0] : g->sc[0]));
+  }
 }
 
 // Work-group barrier that waits for this wave's LDS operations only: global stores
@@ -835,7 +891,9 @@ __device__ __forceinline__ void copy_to_lds(const void* sbase, uint32_t voff, ui
 // rows from a scalar base (the operand pointer plus the K tile's offset), so each copy
 // is one global_load_lds_dwordx4 with a scalar base address.  The host guarantees
 // that every offset of the operand fits in 32 bits.
-template <typename S, int ROWS, int NW, int SIDE>
+// G > 0: the row group has at most G sub-axes, and a row's offset is formed in 32 bits
+// (the same low 32 bits as the 64-bit form).
+template <typename S, int ROWS, int NW, int SIDE, int G = 0>
 struct PipeCopies {
   static constexpr int RPI = 64 / kChunks;  // rows per copy instruction
   static constexpr int NI = ROWS / RPI / NW;
@@ -847,18 +905,30 @@ struct PipeCopies {
     region0 = wave * NI;
     const GroupArgs& g = SIDE == 0 ? p.gm : p.gn;
     const uint32_t lim = (SIDE == 0 ? p.M : p.N) - 1;
+    const uint32_t base = uint32_t(boff * int64_t(sizeof(S)));
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int row = (region0 + i) * RPI + lane / kChunks;
       const int chunk = swz(row, lane % kChunks);
       uint32_t r = row0 + row;
       r = r > lim ? lim : r;  // rows past the edge re-read the last row; never stored
-      off[i] = uint32_t((boff + group_offset<SIDE>(g, r)) * int64_t(sizeof(S))) + uint32_t(chunk * 16);
+      if constexpr (G > 0) off[i] = base + group_offset_d32<SIDE, G>(g, r, sizeof(S)) + uint32_t(chunk * 16);
+      else off[i] = uint32_t((boff + group_offset<SIDE>(g, r)) * int64_t(sizeof(S))) + uint32_t(chunk * 16);
     }
   }
   // copy i of this wave's share of the tile at `base` into the LDS tile at byte address `lds`
   __device__ __forceinline__ void issue_one(int i, const void* base, uint32_t lds) const {
     copy_to_lds(base, off[i], lds + uint32_t((region0 + i) * 1024));
+  }
+  // The same copy through registers (contract_pipe's RSTAGE): the 16 bytes copy i moves
+  // in this lane, loaded into registers (buffer_load_dwordx4 over the operand, `kbytes`
+  // the K tile's byte offset) ...
+  __device__ __forceinline__ uint4 load_one(int i, __amdgpu_buffer_rsrc_t r, uint32_t kbytes) const {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off[i], kbytes, 0));
+  }
+  // ... and written where the copy puts them (16 * lane bytes into the copy's 1 KB region)
+  __device__ __forceinline__ void store_one(int i, const uint4& v, S* tile, int lane) const {
+    *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tile) + (region0 + i) * 1024 + lane * 16) = v;
   }
 };
 
@@ -960,7 +1030,7 @@ struct PipeCopiesHalo {
 // of 8); they are never stored.
 __device__ __forceinline__ int mn_swz(int r) { return (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2); }
 
-template <typename S, int ROWS, int NW, int SIDE>
+template <typename S, int ROWS, int NW, int SIDE, int G = 0>
 struct PipeCopiesMN {
   static constexpr int NI = ROWS / 8 / NW;  // 1 KB copies of this wave per K tile
   static_assert(NI >= 1 && ROWS % (8 * NW) == 0 && ROWS % 64 == 0, "tile shape");
@@ -979,7 +1049,7 @@ struct PipeCopiesMN {
       const int chunk = (lane % 8) ^ mn_swz(kr);
       uint32_t r = row0 + uint32_t((q / 8) * 64 + chunk * 8);
       r = r > last ? last : r;
-      off[i] = uint32_t((boff + group_offset<SIDE>(g, r) + int64_t(kr) * kstride) * int64_t(sizeof(S)));
+      off[i] = uint32_t((boff + group_offset_d<SIDE, G>(g, r) + int64_t(kr) * kstride) * int64_t(sizeof(S)));
     }
   }
   __device__ __forceinline__ void issue_one(int i, const void* base, uint32_t lds) const {
@@ -1117,7 +1187,7 @@ __device__ __forceinline__ void pipe_drain(f32x4 (&acc)[FM][FN]) {
 // the whole work-group writes the rows out (16-byte streaming stores along n when n is
 // the output's contiguous axis, element stores otherwise).  The caller has drained
 // every copy into LDS and synchronised the work-group.
-template <typename T, int BN, int FM, int FN, bool BIAS>
+template <typename T, int BN, int FM, int FN, bool BIAS, int G = 0>
 __device__ __forceinline__ void store_pipe(const ContractArgs& p, typename Traits<T>::S* lds0,
                                            typename Traits<T>::S* lds1, const f32x4 (&acc)[FM][FN], uint32_t m0,
                                            uint32_t n0, int64_t boff_c) {
@@ -1142,11 +1212,11 @@ __device__ __forceinline__ void store_pipe(const ContractArgs& p, typename Trait
   const KArgs kp = kernel_args();
   for (int r = tid; r < BM; r += NT) {
     const uint32_t m = m0 + r;
-    row_off[r] = m < p.M ? boff_c + group_offset_k<2>(&kp->gm, m) : -1;
+    row_off[r] = m < p.M ? boff_c + group_offset_kd<2, G>(&kp->gm, m) : -1;
   }
   for (int c = tid; c < BN; c += NT) {
     const uint32_t n = n0 + c;
-    col_off[c] = n < p.N ? group_offset_k<2>(&kp->gn, n) : -1;
+    col_off[c] = n < p.N ? group_offset_kd<2, G>(&kp->gn, n) : -1;
   }
   // BIAS: the bias of this lane's columns (es_contract_bias), added before the one rounding
   f32x4 bv[FN];
@@ -1207,7 +1277,7 @@ __device__ __forceinline__ void store_pipe(const ContractArgs& p, typename Trait
 // c sits at c ^ (r % 32) (the 8-byte writes of 16 rows and the 16-byte reads along a
 // row then spread over all banks); one barrier; the whole work-group writes the tile
 // with 16-byte streaming stores.  The offset tables have 4 KB of LDS of their own.
-template <typename T, int FM, int FN, bool BIAS>
+template <typename T, int FM, int FN, bool BIAS, int G = 0>
 __device__ __forceinline__ void store_pipe_wide(const ContractArgs& p, typename Traits<T>::S* lds0,
                                                 typename Traits<T>::S* lds1, const f32x4 (&acc)[FM][FN],
                                                 uint32_t m0, uint32_t n0, int64_t boff_c) {
@@ -1233,8 +1303,8 @@ __device__ __forceinline__ void store_pipe_wide(const ContractArgs& p, typename 
   const KArgs kp = kernel_args();
   {
     const uint32_t m = m0 + tid, n = n0 + tid;
-    row_off[tid] = m < p.M ? boff_c + group_offset_k<2>(&kp->gm, m) : -1;
-    col_off[tid] = n < p.N ? group_offset_k<2>(&kp->gn, n) : -1;
+    row_off[tid] = m < p.M ? boff_c + group_offset_kd<2, G>(&kp->gm, m) : -1;
+    col_off[tid] = n < p.N ? group_offset_kd<2, G>(&kp->gn, n) : -1;
   }
   S* region = wm == 0 ? lds0 : lds1;
 #pragma unroll
@@ -1268,7 +1338,7 @@ __device__ __forceinline__ void store_pipe_wide(const ContractArgs& p, typename 
 // [column n][row m], and written with 16-byte streaming stores along m.  A lane's four
 // consecutive-n values go to four staged rows (four 2-byte LDS writes).  Passes and
 // tables as in store_pipe, sized for the transposed stage.
-template <typename T, int BN, int FM, int FN, bool BIAS>
+template <typename T, int BN, int FM, int FN, bool BIAS, int G = 0>
 __device__ __forceinline__ void store_pipe_t(const ContractArgs& p, typename Traits<T>::S* lds0,
                                              typename Traits<T>::S* lds1, const f32x4 (&acc)[FM][FN], uint32_t m0,
                                              uint32_t n0, int64_t boff_c) {
@@ -1294,11 +1364,11 @@ __device__ __forceinline__ void store_pipe_t(const ContractArgs& p, typename Tra
   const KArgs kp = kernel_args();
   for (int r = tid; r < BM; r += NT) {
     const uint32_t m = m0 + r;
-    row_off[r] = m < p.M ? boff_c + group_offset_k<2>(&kp->gm, m) : -1;
+    row_off[r] = m < p.M ? boff_c + group_offset_kd<2, G>(&kp->gm, m) : -1;
   }
   for (int c = tid; c < BN; c += NT) {
     const uint32_t n = n0 + c;
-    col_off[c] = n < p.N ? group_offset_k<2>(&kp->gn, n) : -1;
+    col_off[c] = n < p.N ? group_offset_kd<2, G>(&kp->gn, n) : -1;
   }
   f32x4 bv[FN];
 #pragma unroll
@@ -1343,7 +1413,7 @@ __device__ __forceinline__ void store_pipe_t(const ContractArgs& p, typename Tra
 // store_tile_f32, for the 16 x 16 blocks of v_mfma_f32_16x16x32, whose acc[i][j] holds
 // columns wn*WTN + j*16 + 4*(lane/16) + 0..3 of tile row wm*128 + i*16 + lane%16.  The
 // offset tables sit at the start of the two (free) stages.
-template <typename T, int BN, int FM, int FN, bool BIAS, bool VEC_ONLY = false>
+template <typename T, int BN, int FM, int FN, bool BIAS, bool VEC_ONLY = false, int G = 0>
 __device__ __forceinline__ void store_pipe_f32(const ContractArgs& p, typename Traits<T>::S* lds0,
                                                typename Traits<T>::S* lds1, const f32x4 (&acc)[FM][FN],
                                                uint32_t m0, uint32_t n0, int64_t boff_c) {
@@ -1360,11 +1430,11 @@ __device__ __forceinline__ void store_pipe_f32(const ContractArgs& p, typename T
   const KArgs kp = kernel_args();
   for (int r = tid; r < BM; r += NT) {
     const uint32_t m = m0 + r;
-    row_off[r] = m < p.M ? boff_c + group_offset_k<2>(&kp->gm, m) : -1;
+    row_off[r] = m < p.M ? boff_c + group_offset_kd<2, G>(&kp->gm, m) : -1;
   }
   for (int c = tid; c < BN; c += NT) {
     const uint32_t n = n0 + c;
-    col_off[c] = n < p.N ? group_offset_k<2>(&kp->gn, n) : -1;
+    col_off[c] = n < p.N ? group_offset_kd<2, G>(&kp->gn, n) : -1;
   }
   lds_barrier();
 #pragma unroll
@@ -1403,7 +1473,15 @@ __device__ __forceinline__ void store_pipe_f32(const ContractArgs& p, typename T
 // 1 and 2 is an instantiation of its own: with every epilogue in one function the
 // 256-wide kernel spilled accumulators to scratch.
 // HALO: A is read by PipeCopiesHalo (es_contract_halo), both operands K-contiguous.
-template <typename T, int BN, int L, int LA, int LB, int EPI = 0, bool HALO = false>
+// G > 0: the batch, M and N groups have at most G sub-axes each (ContractArgs::gdims, no
+// halo): every row, column and batch offset is an unrolled walk of G - 1 divisions, so the
+// set-up in front of the first copies is a few hundred instructions instead of a walk over
+// ES_MAX_AXES sub-axes per row with a scalar load per step.
+// RSTAGE: K-contiguous operands are copied through registers (global_load_dwordx4, then
+// ds_write_b128) instead of by LDS-DMA: the loads of K tile kt+2 are issued in step kt's
+// second substep, their writes into the free stage spread over step kt+1's first.
+template <typename T, int BN, int L, int LA, int LB, int EPI = 0, bool HALO = false, int G = 0,
+          bool RSTAGE = false>
 __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   using S = typename Traits<T>::S;
   constexpr int BM = 256, WM = 2, WN = 2;
@@ -1416,9 +1494,12 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   constexpr int MMAS = FM * FN;  // per substep
   using CopyA = std::conditional_t<
       HALO, PipeCopiesHalo<S, BM, WM * WN>,
-      std::conditional_t<LA == kMNContig, PipeCopiesMN<S, BM, WM * WN, 0>, PipeCopies<S, BM, WM * WN, 0>>>;
+      std::conditional_t<LA == kMNContig, PipeCopiesMN<S, BM, WM * WN, 0, G>, PipeCopies<S, BM, WM * WN, 0, G>>>;
   static_assert(!HALO || (LA == kKContig && LB == kKContig), "the halo reads K-contiguous operands");
-  using CopyB = std::conditional_t<LB == kMNContig, PipeCopiesMN<S, BN, WM * WN, 1>, PipeCopies<S, BN, WM * WN, 1>>;
+  static_assert(G == 0 || !HALO, "the halo copies walk the M group themselves");
+  static_assert(!RSTAGE || (!HALO && LA == kKContig && LB == kKContig), "register staging reads K-contiguous operands");
+  using CopyB =
+      std::conditional_t<LB == kMNContig, PipeCopiesMN<S, BN, WM * WN, 1, G>, PipeCopies<S, BN, WM * WN, 1, G>>;
   using FragA = PipeFrag<S, LA>;
   using FragB = PipeFrag<S, LB>;
   constexpr int NREAD = FM * FragA::READS + FN * FragB::READS;  // LDS read instructions per substep
@@ -1441,9 +1522,9 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   tile_of(p, blockIdx.x, bidx, tm, tn);
   const uint32_t m0 = tm * BM;
   const uint32_t n0 = tn * BN;
-  const int64_t boff_a = group_offset<0>(p.gb, bidx);
-  const int64_t boff_b = group_offset<1>(p.gb, bidx);
-  const int64_t boff_c = group_offset<2>(p.gb, bidx);
+  const int64_t boff_a = group_offset_d<0, G>(p.gb, bidx);
+  const int64_t boff_b = group_offset_d<1, G>(p.gb, bidx);
+  const int64_t boff_c = group_offset_d<2, G>(p.gb, bidx);
 
   CopyA ca;
   CopyB cb;
@@ -1500,20 +1581,50 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
       cb.issue_one(q - CopyA::NI, static_cast<const S*>(p.b) + w.ob, stage + uint32_t(BM * BK * sizeof(S)));
     }
   };
-  halo_voffs();
+  // RSTAGE: the staged copies of the next K tile, loaded through buffer resources over A
+  // and B (the range is the whole 32-bit offset space: every offset of an operand fits)
+  uint4 rs[RSTAGE ? NCOPY : 1];
+  const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.a), 0, -1, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.b), 0, -1, 0x00020000);
+  auto rload = [&](int q) {
+    if constexpr (RSTAGE) {
+      if (q < CopyA::NI) rs[q] = ca.load_one(q, rsrc_a, uint32_t(w.oa) * uint32_t(sizeof(S)));
+      else rs[q] = cb.load_one(q - CopyA::NI, rsrc_b, uint32_t(w.ob) * uint32_t(sizeof(S)));
+    }
+  };
+  auto rstore = [&](int q, S* stage) {
+    if constexpr (RSTAGE) {
+      if (q < CopyA::NI) ca.store_one(q, rs[q], stage, lane);
+      else cb.store_one(q - CopyA::NI, rs[q], stage + BM * BK, lane);
+    }
+  };
+  if constexpr (RSTAGE) {
+    // K tile 0 into stage 0; K tile 1 stays in registers for the first step to write
 #pragma unroll
-  for (int q = 0; q < NCOPY; ++q) copy(q, lds0_addr);
-  w.advance(nk);
-  halo_voffs();
+    for (int q = 0; q < NCOPY; ++q) rload(q);
+    w.advance(nk);
 #pragma unroll
-  for (int q = 0; q < NCOPY; ++q) copy(q, lds1_addr);
-  w.advance(nk);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY) : "memory");  // K tile 0 of this wave landed
+    for (int q = 0; q < NCOPY; ++q) rstore(q, lds0);
+#pragma unroll
+    for (int q = 0; q < NCOPY; ++q) rload(q);
+    w.advance(nk);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  } else {
+    halo_voffs();
+#pragma unroll
+    for (int q = 0; q < NCOPY; ++q) copy(q, lds0_addr);
+    w.advance(nk);
+    halo_voffs();
+#pragma unroll
+    for (int q = 0; q < NCOPY; ++q) copy(q, lds1_addr);
+    w.advance(nk);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY) : "memory");  // K tile 0 of this wave landed
+  }
   __syncthreads();
   frags(lds0, 0, 0);
 
   // first: the tile's first K tile, whose first MFMAs start the accumulators from 0
-  auto step = [&](S* stage_cur, const S* stage_nxt, uint32_t cur_addr, auto first) {
+  auto step = [&](S* stage_cur, S* stage_nxt, uint32_t cur_addr, auto first) {
     // substep 0: its MFMAs interleaved with the fragment reads of substep 1 (HALO: and
     // with the offsets of the copies substep 1 issues, one per MFMA from the first)
     const uint32_t tap = halo_tap();
@@ -1529,10 +1640,16 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
         if (r0 < FM) af[1][r0] = fa.read(stage_cur, r0, 1);
         else bf[1][r0 - FM] = fb.read(stage_cur + BM * BK, r0 - FM, 1);
       }
+      // RSTAGE: K tile kt+1 from registers into its stage (free since the last barrier)
+      if constexpr (RSTAGE) {
+        const int c0 = (q * NCOPY) / MMAS, c1 = ((q + 1) * NCOPY) / MMAS;
+        if (c0 != c1) rstore(c0, stage_nxt);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
     // K tile kt+1 complete for everyone; every read of stage kt done
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if constexpr (RSTAGE) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     // substep 1: its MFMAs, the copies of K tile kt+2 into this stage and the first
     // fragments of K tile kt+1, interleaved in program order
@@ -1541,7 +1658,10 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
       PipeMma<T>::mma(acc[q / FN][q % FN], bf[1][q % FN], af[1][q / FN]);
       // copies and fragment reads spread evenly over the substep, alternating
       const int c0 = (q * NCOPY) / MMAS, c1 = ((q + 1) * NCOPY) / MMAS;
-      if (c0 != c1) copy(c0, cur_addr);
+      if (c0 != c1) {
+        if constexpr (RSTAGE) rload(c0);
+        else copy(c0, cur_addr);
+      }
       const int r0 = (q * (FM + FN)) / MMAS, r1 = ((q + 1) * (FM + FN)) / MMAS;
       if (r0 != r1) {
         if (r0 < FM) af[0][r0] = fa.read(stage_nxt, r0, 0);
@@ -1565,23 +1685,23 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   __syncthreads();
   if constexpr (EPI == 1) {
     static_assert(BN == 256, "the one-pass epilogue stages 256-wide tiles");
-    if (p.bias != nullptr) store_pipe_wide<T, FM, FN, true>(p, lds0, lds1, acc, m0, n0, boff_c);
-    else store_pipe_wide<T, FM, FN, false>(p, lds0, lds1, acc, m0, n0, boff_c);
+    if (p.bias != nullptr) store_pipe_wide<T, FM, FN, true, G>(p, lds0, lds1, acc, m0, n0, boff_c);
+    else store_pipe_wide<T, FM, FN, false, G>(p, lds0, lds1, acc, m0, n0, boff_c);
     return;
   }
   if constexpr (EPI == 2) {  // fp32 output with vector stores and no bias (split-K partials)
-    store_pipe_f32<T, BN, FM, FN, false, true>(p, lds0, lds1, acc, m0, n0, boff_c);
+    store_pipe_f32<T, BN, FM, FN, false, true, G>(p, lds0, lds1, acc, m0, n0, boff_c);
     return;
   }
   if (p.out_f32) {
-    if (p.bias != nullptr) store_pipe_f32<T, BN, FM, FN, true>(p, lds0, lds1, acc, m0, n0, boff_c);
-    else store_pipe_f32<T, BN, FM, FN, false>(p, lds0, lds1, acc, m0, n0, boff_c);
+    if (p.bias != nullptr) store_pipe_f32<T, BN, FM, FN, true, false, G>(p, lds0, lds1, acc, m0, n0, boff_c);
+    else store_pipe_f32<T, BN, FM, FN, false, false, G>(p, lds0, lds1, acc, m0, n0, boff_c);
   } else if (p.vstore == 2) {
-    if (p.bias != nullptr) store_pipe_t<T, BN, FM, FN, true>(p, lds0, lds1, acc, m0, n0, boff_c);
-    else store_pipe_t<T, BN, FM, FN, false>(p, lds0, lds1, acc, m0, n0, boff_c);
+    if (p.bias != nullptr) store_pipe_t<T, BN, FM, FN, true, G>(p, lds0, lds1, acc, m0, n0, boff_c);
+    else store_pipe_t<T, BN, FM, FN, false, G>(p, lds0, lds1, acc, m0, n0, boff_c);
   } else {
-    if (p.bias != nullptr) store_pipe<T, BN, FM, FN, true>(p, lds0, lds1, acc, m0, n0, boff_c);
-    else store_pipe<T, BN, FM, FN, false>(p, lds0, lds1, acc, m0, n0, boff_c);
+    if (p.bias != nullptr) store_pipe<T, BN, FM, FN, true, G>(p, lds0, lds1, acc, m0, n0, boff_c);
+    else store_pipe<T, BN, FM, FN, false, G>(p, lds0, lds1, acc, m0, n0, boff_c);
   }
 }
 
@@ -1844,6 +1964,43 @@ void launch_pipe_halo(const ContractArgs& p, hipStream_t s) {
   else contract_pipe<T, BN, kKLevels, kKContig, kKContig, EPI, true><<<p.total_tiles, 256, 0, s>>>(p);
 }
 
+// The bounded-group instantiations (ContractArgs::gdims: at most G sub-axes per batch,
+// M and N group; at most two K levels): the 224-wide tile, and the 256-wide tile's two
+// one-pass epilogues (16-bit output with vector stores along n; fp32 split-K partials).
+// Returns false when the call takes the generic instantiations instead.
+template <typename T, int BN, int LA, int LB, int G>
+bool launch_pipe_g(const ContractArgs& p, hipStream_t s) {
+  const bool l1 = p.klevels == 1;
+  if constexpr (BN == 256) {
+    if (p.out_f32 && p.vstore == 1 && p.bias == nullptr) {
+      if (l1) contract_pipe<T, BN, 1, LA, LB, 2, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+      else contract_pipe<T, BN, 2, LA, LB, 2, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+      return true;
+    }
+    if (p.vstore == 1 && !p.out_f32) {
+      if (l1) contract_pipe<T, BN, 1, LA, LB, 1, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+      else contract_pipe<T, BN, 2, LA, LB, 1, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+      return true;
+    }
+    return false;
+  } else {
+    if (l1) contract_pipe<T, BN, 1, LA, LB, 0, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+    else contract_pipe<T, BN, 2, LA, LB, 0, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+    return true;
+  }
+}
+
+// one sub-axis per group (the plain GEMM x[M, K] w[N, K], both operands K-contiguous)
+// takes G = 1, where a row's offset is one multiply; up to two take G = 2
+template <typename T, int BN, int LA, int LB>
+bool launch_pipe_bounded(const ContractArgs& p, hipStream_t s) {
+  if (p.gdims == 0 || p.klevels > 2) return false;
+  if constexpr (LA == kKContig && LB == kKContig) {
+    if (p.gdims == 1) return launch_pipe_g<T, BN, LA, LB, 1>(p, s);
+  }
+  return launch_pipe_g<T, BN, LA, LB, 2>(p, s);
+}
+
 template <typename T, int BN, int LA, int LB>
 void launch_pipe(const ContractArgs& p, hipStream_t s) {
   if constexpr (LA == kKContig && LB == kKContig) {
@@ -1857,6 +2014,7 @@ void launch_pipe(const ContractArgs& p, hipStream_t s) {
       return;
     }
   }
+  if (launch_pipe_bounded<T, BN, LA, LB>(p, s)) return;
   if constexpr (BN == 256) {
     if (p.out_f32 && p.vstore == 1 && p.bias == nullptr) {
       switch (p.klevels) {
