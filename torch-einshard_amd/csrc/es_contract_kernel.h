@@ -920,16 +920,6 @@ struct PipeCopies {
   __device__ __forceinline__ void issue_one(int i, const void* base, uint32_t lds) const {
     copy_to_lds(base, off[i], lds + uint32_t((region0 + i) * 1024));
   }
-  // The same copy through registers (contract_pipe's RSTAGE): the 16 bytes copy i moves
-  // in this lane, loaded into registers (buffer_load_dwordx4 over the operand, `kbytes`
-  // the K tile's byte offset) ...
-  __device__ __forceinline__ uint4 load_one(int i, __amdgpu_buffer_rsrc_t r, uint32_t kbytes) const {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off[i], kbytes, 0));
-  }
-  // ... and written where the copy puts them (16 * lane bytes into the copy's 1 KB region)
-  __device__ __forceinline__ void store_one(int i, const uint4& v, S* tile, int lane) const {
-    *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tile) + (region0 + i) * 1024 + lane * 16) = v;
-  }
 };
 
 // The same copy through a buffer resource (es_contract_halo): lane l moves 16 bytes
@@ -1477,11 +1467,7 @@ __device__ __forceinline__ void store_pipe_f32(const ContractArgs& p, typename T
 // halo): every row, column and batch offset is an unrolled walk of G - 1 divisions, so the
 // set-up in front of the first copies is a few hundred instructions instead of a walk over
 // ES_MAX_AXES sub-axes per row with a scalar load per step.
-// RSTAGE: K-contiguous operands are copied through registers (global_load_dwordx4, then
-// ds_write_b128) instead of by LDS-DMA: the loads of K tile kt+2 are issued in step kt's
-// second substep, their writes into the free stage spread over step kt+1's first.
-template <typename T, int BN, int L, int LA, int LB, int EPI = 0, bool HALO = false, int G = 0,
-          bool RSTAGE = false>
+template <typename T, int BN, int L, int LA, int LB, int EPI = 0, bool HALO = false, int G = 0>
 __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   using S = typename Traits<T>::S;
   constexpr int BM = 256, WM = 2, WN = 2;
@@ -1497,7 +1483,6 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
       std::conditional_t<LA == kMNContig, PipeCopiesMN<S, BM, WM * WN, 0, G>, PipeCopies<S, BM, WM * WN, 0, G>>>;
   static_assert(!HALO || (LA == kKContig && LB == kKContig), "the halo reads K-contiguous operands");
   static_assert(G == 0 || !HALO, "the halo copies walk the M group themselves");
-  static_assert(!RSTAGE || (!HALO && LA == kKContig && LB == kKContig), "register staging reads K-contiguous operands");
   using CopyB =
       std::conditional_t<LB == kMNContig, PipeCopiesMN<S, BN, WM * WN, 1, G>, PipeCopies<S, BN, WM * WN, 1, G>>;
   using FragA = PipeFrag<S, LA>;
@@ -1581,50 +1566,20 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
       cb.issue_one(q - CopyA::NI, static_cast<const S*>(p.b) + w.ob, stage + uint32_t(BM * BK * sizeof(S)));
     }
   };
-  // RSTAGE: the staged copies of the next K tile, loaded through buffer resources over A
-  // and B (the range is the whole 32-bit offset space: every offset of an operand fits)
-  uint4 rs[RSTAGE ? NCOPY : 1];
-  const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.a), 0, -1, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.b), 0, -1, 0x00020000);
-  auto rload = [&](int q) {
-    if constexpr (RSTAGE) {
-      if (q < CopyA::NI) rs[q] = ca.load_one(q, rsrc_a, uint32_t(w.oa) * uint32_t(sizeof(S)));
-      else rs[q] = cb.load_one(q - CopyA::NI, rsrc_b, uint32_t(w.ob) * uint32_t(sizeof(S)));
-    }
-  };
-  auto rstore = [&](int q, S* stage) {
-    if constexpr (RSTAGE) {
-      if (q < CopyA::NI) ca.store_one(q, rs[q], stage, lane);
-      else cb.store_one(q - CopyA::NI, rs[q], stage + BM * BK, lane);
-    }
-  };
-  if constexpr (RSTAGE) {
-    // K tile 0 into stage 0; K tile 1 stays in registers for the first step to write
+  halo_voffs();
 #pragma unroll
-    for (int q = 0; q < NCOPY; ++q) rload(q);
-    w.advance(nk);
+  for (int q = 0; q < NCOPY; ++q) copy(q, lds0_addr);
+  w.advance(nk);
+  halo_voffs();
 #pragma unroll
-    for (int q = 0; q < NCOPY; ++q) rstore(q, lds0);
-#pragma unroll
-    for (int q = 0; q < NCOPY; ++q) rload(q);
-    w.advance(nk);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  } else {
-    halo_voffs();
-#pragma unroll
-    for (int q = 0; q < NCOPY; ++q) copy(q, lds0_addr);
-    w.advance(nk);
-    halo_voffs();
-#pragma unroll
-    for (int q = 0; q < NCOPY; ++q) copy(q, lds1_addr);
-    w.advance(nk);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY) : "memory");  // K tile 0 of this wave landed
-  }
+  for (int q = 0; q < NCOPY; ++q) copy(q, lds1_addr);
+  w.advance(nk);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY) : "memory");  // K tile 0 of this wave landed
   __syncthreads();
   frags(lds0, 0, 0);
 
   // first: the tile's first K tile, whose first MFMAs start the accumulators from 0
-  auto step = [&](S* stage_cur, S* stage_nxt, uint32_t cur_addr, auto first) {
+  auto step = [&](S* stage_cur, const S* stage_nxt, uint32_t cur_addr, auto first) {
     // substep 0: its MFMAs interleaved with the fragment reads of substep 1 (HALO: and
     // with the offsets of the copies substep 1 issues, one per MFMA from the first)
     const uint32_t tap = halo_tap();
@@ -1640,16 +1595,10 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
         if (r0 < FM) af[1][r0] = fa.read(stage_cur, r0, 1);
         else bf[1][r0 - FM] = fb.read(stage_cur + BM * BK, r0 - FM, 1);
       }
-      // RSTAGE: K tile kt+1 from registers into its stage (free since the last barrier)
-      if constexpr (RSTAGE) {
-        const int c0 = (q * NCOPY) / MMAS, c1 = ((q + 1) * NCOPY) / MMAS;
-        if (c0 != c1) rstore(c0, stage_nxt);
-      }
     }
     __builtin_amdgcn_sched_barrier(0);
     // K tile kt+1 complete for everyone; every read of stage kt done
-    if constexpr (RSTAGE) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     // substep 1: its MFMAs, the copies of K tile kt+2 into this stage and the first
     // fragments of K tile kt+1, interleaved in program order
@@ -1658,10 +1607,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
       PipeMma<T>::mma(acc[q / FN][q % FN], bf[1][q % FN], af[1][q / FN]);
       // copies and fragment reads spread evenly over the substep, alternating
       const int c0 = (q * NCOPY) / MMAS, c1 = ((q + 1) * NCOPY) / MMAS;
-      if (c0 != c1) {
-        if constexpr (RSTAGE) rload(c0);
-        else copy(c0, cur_addr);
-      }
+      if (c0 != c1) copy(c0, cur_addr);
       const int r0 = (q * (FM + FN)) / MMAS, r1 = ((q + 1) * (FM + FN)) / MMAS;
       if (r0 != r1) {
         if (r0 < FM) af[0][r0] = fa.read(stage_nxt, r0, 0);
