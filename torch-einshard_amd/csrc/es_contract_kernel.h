@@ -1258,24 +1258,30 @@ __device__ __forceinline__ void store_pipe(const ContractArgs& p, typename Trait
   }
 }
 
-// The epilogue of contract_pipe's 256-wide tiles when n is the output's contiguous axis
-// (vstore == 1) and the output is 16-bit: a kernel instantiation of its own (EPI == 1),
-// since with every epilogue in one function the register allocator spilled 36
-// accumulator registers to scratch, about 6 us per launch.  One pass: each accumulator
-// is rounded (after the bias) and written to the two freed stages, wave row 0's 128
-// rows in stage 0 and wave row 1's in stage 1, as rows of 512 bytes whose 16-byte chunk
-// c sits at c ^ (r % 32) (the 8-byte writes of 16 rows and the 16-byte reads along a
-// row then spread over all banks); one barrier; the whole work-group writes the tile
-// with 16-byte streaming stores.  The offset tables have 4 KB of LDS of their own.
-template <typename T, int FM, int FN, bool BIAS, int G = 0>
+// The epilogue of contract_pipe when n is the output's contiguous axis (vstore == 1)
+// and the output is 16-bit: a kernel instantiation of its own (EPI == 1), since with
+// every epilogue in one function the register allocator spilled 36 accumulator
+// registers of the 256-wide tile to scratch, about 6 us per launch.  One pass: each
+// accumulator is rounded (after the bias) and written to the two freed stages, wave row
+// 0's 128 rows in stage 0 and wave row 1's in stage 1, as rows of 512 bytes (a 224-wide
+// tile leaves 4 chunks of each unused) whose 16-byte chunk c sits at c ^ (r % 32): the
+// 8-byte writes of 16 rows and the 16-byte reads along a row then spread over all banks
+// (the padded rows of store_pipe, 464 bytes apart, measured 2.0-2.3 us of tables and
+// staging per 224-wide tile on C4); one barrier; the whole work-group writes the tile
+// with 16-byte streaming stores.  The offset tables (`tables`, BM + 256 entries) have
+// 4 KB of LDS of their own; PRE: the caller formed them before its K loop (as here), so
+// the epilogue reads no kernel argument (after 100 us of K loop such a scalar load misses
+// every cache, and a few of them in a row measured 1-2 us per tile).  C is the output.
+template <typename T, int BN, int FM, int FN, bool BIAS, int G = 0, bool PRE = false>
 __device__ __forceinline__ void store_pipe_wide(const ContractArgs& p, typename Traits<T>::S* lds0,
                                                 typename Traits<T>::S* lds1, const f32x4 (&acc)[FM][FN],
-                                                uint32_t m0, uint32_t n0, int64_t boff_c) {
+                                                uint32_t m0, uint32_t n0, int64_t boff_c, int64_t* tables,
+                                                typename Traits<T>::S* C) {
   using S = typename Traits<T>::S;
-  constexpr int BM = 256, BN = 256, WTN = 128, NT = 256, VEC = 8;
+  constexpr int BM = 256, WTN = BN / 2, NT = 256, VEC = 8;
+  constexpr int SP = 256;       // staged row pitch (elements): 32 chunks
   constexpr int CH = BN / VEC;  // 16-byte chunks per row
-  static_assert(FM * 16 == 128 && FN * 16 == WTN, "256 x 256 tiles of four 128 x 128 waves");
-  __shared__ int64_t tables[BM + BN];
+  static_assert(FM * 16 == 128 && FN * 16 == WTN && BN <= SP, "256 x BN tiles of four 128 x BN/2 waves");
   int64_t* row_off = tables;
   int64_t* col_off = tables + BM;
   const int tid = threadIdx.x;
@@ -1283,18 +1289,17 @@ __device__ __forceinline__ void store_pipe_wide(const ContractArgs& p, typename 
   const int wave = tid / 64;
   const int wm = wave / 2;
   const int wn = wave % 2;
-  S* C = static_cast<S*>(p.c);
   // the bias loads go first, so their latency passes while the offset tables are formed
   f32x4 bv[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j)
 #pragma unroll
     for (int r = 0; r < 4; ++r) bv[j][r] = BIAS ? bias_at<T>(p, n0 + wn * WTN + j * 16 + 4 * (lane / 16) + r) : 0.f;
-  const KArgs kp = kernel_args();
-  {
+  if constexpr (!PRE) {
+    const KArgs kp = kernel_args();
     const uint32_t m = m0 + tid, n = n0 + tid;
     row_off[tid] = m < p.M ? boff_c + group_offset_kd<2, G>(&kp->gm, m) : -1;
-    col_off[tid] = n < p.N ? group_offset_kd<2, G>(&kp->gn, n) : -1;
+    if (tid < BN) col_off[tid] = n < p.N ? group_offset_kd<2, G>(&kp->gn, n) : -1;
   }
   S* region = wm == 0 ? lds0 : lds1;
 #pragma unroll
@@ -1304,7 +1309,7 @@ __device__ __forceinline__ void store_pipe_wide(const ContractArgs& p, typename 
     for (int i = 0; i < FM; ++i) {
       const int r = i * 16 + lane % 16;  // row within the stage
       const f32x4 a = BIAS ? acc[i][j] + bv[j] : acc[i][j];
-      *reinterpret_cast<uint2*>(region + r * BN + ((col / VEC) ^ (r % 32)) * VEC + col % VEC) =
+      *reinterpret_cast<uint2*>(region + r * SP + ((col / VEC) ^ (r % 32)) * VEC + col % VEC) =
           uint2{Traits<T>::pack2(a[0], a[1]), Traits<T>::pack2(a[2], a[3])};
     }
   }
@@ -1318,7 +1323,7 @@ __device__ __forceinline__ void store_pipe_wide(const ContractArgs& p, typename 
     // nontemporal: the output is not read again by this kernel, so it is not kept in L2
     if (ro >= 0 && co >= 0)
       __builtin_nontemporal_store(
-          *reinterpret_cast<const u32x4*>((row < 128 ? lds0 : lds1) + rr * BN + (cv ^ (rr % 32)) * VEC),
+          *reinterpret_cast<const u32x4*>((row < 128 ? lds0 : lds1) + rr * SP + (cv ^ (rr % 32)) * VEC),
           reinterpret_cast<u32x4*>(C + ro + co));
   }
 }
@@ -1457,7 +1462,8 @@ __device__ __forceinline__ void store_pipe_f32(const ContractArgs& p, typename T
 }
 
 // EPI: 0 = the epilogue chosen at run time (fp32, transposed, vector or element stores);
-// 1 = 256-wide tiles with vector stores along n and a 16-bit output (store_pipe_wide);
+// 1 = vector stores along n and a 16-bit output (store_pipe_wide; a 224-wide tile's
+// stages are then sized for its 512-byte staged rows);
 // 2 = 256-wide tiles with an fp32 output, vector stores along n and no bias (split-K
 // partials, store_pipe_f32).  Each of
 // 1 and 2 is an instantiation of its own: with every epilogue in one function the
@@ -1494,8 +1500,16 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   static_assert(NCOPY <= MMAS && NREAD <= MMAS, "last substep interleave");
   static_assert((LA == kKContig || WTM % 64 == 0) && (LB == kKContig || WTN % 64 == 0), "MN blocks of 64 rows");
 
-  __shared__ __attribute__((aligned(1024))) S lds0[STAGE];
-  __shared__ __attribute__((aligned(1024))) S lds1[STAGE];
+  // EPI 1 stages 128 rows of 256 elements per stage (more than a 224-wide tile's K stage)
+  constexpr int STAGE_ALLOC = EPI == 1 && STAGE < 128 * 256 ? 128 * 256 : STAGE;
+  __shared__ __attribute__((aligned(1024))) S lds0[STAGE_ALLOC];
+  __shared__ __attribute__((aligned(1024))) S lds1[STAGE_ALLOC];
+  // the one-pass epilogue's row and column offset tables
+  __shared__ int64_t ep_tables[EPI == 1 ? BM + 256 : 1];
+  // EPI 1 with bounded groups forms those tables in the prologue (while the first copies
+  // are in flight) and keeps the output pointer and the bias test in scalar registers
+  // through the K loop: the epilogue then reads no kernel argument
+  constexpr bool kPreTables = EPI == 1 && G > 0;
 
   const int tid = threadIdx.x;
   const int lane = tid % 64;
@@ -1574,6 +1588,19 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
 #pragma unroll
   for (int q = 0; q < NCOPY; ++q) copy(q, lds1_addr);
   w.advance(nk);
+  S* out_c = static_cast<S*>(p.c);
+  uint32_t has_bias = p.bias != nullptr ? 1u : 0u;
+  if constexpr (kPreTables) {
+    const uint32_t m = m0 + tid, n = n0 + tid;
+    ep_tables[tid] = m < p.M ? boff_c + group_offset_d<2, G>(p.gm, m) : -1;
+    if (tid < BN) ep_tables[BM + tid] = n < p.N ? group_offset_d<2, G>(p.gn, n) : -1;
+    const uint64_t cbits = reinterpret_cast<uint64_t>(out_c);
+    uint32_t clo = __builtin_amdgcn_readfirstlane(uint32_t(cbits));
+    uint32_t chi = __builtin_amdgcn_readfirstlane(uint32_t(cbits >> 32));
+    has_bias = __builtin_amdgcn_readfirstlane(has_bias);
+    asm volatile("" : "+s"(clo), "+s"(chi), "+s"(has_bias));
+    out_c = reinterpret_cast<S*>((uint64_t(chi) << 32) | clo);
+  }
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY) : "memory");  // K tile 0 of this wave landed
   __syncthreads();
   frags(lds0, 0, 0);
@@ -1630,9 +1657,10 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if constexpr (EPI == 1) {
-    static_assert(BN == 256, "the one-pass epilogue stages 256-wide tiles");
-    if (p.bias != nullptr) store_pipe_wide<T, FM, FN, true, G>(p, lds0, lds1, acc, m0, n0, boff_c);
-    else store_pipe_wide<T, FM, FN, false, G>(p, lds0, lds1, acc, m0, n0, boff_c);
+    if (has_bias)
+      store_pipe_wide<T, BN, FM, FN, true, G, kPreTables>(p, lds0, lds1, acc, m0, n0, boff_c, ep_tables, out_c);
+    else
+      store_pipe_wide<T, BN, FM, FN, false, G, kPreTables>(p, lds0, lds1, acc, m0, n0, boff_c, ep_tables, out_c);
     return;
   }
   if constexpr (EPI == 2) {  // fp32 output with vector stores and no bias (split-K partials)
@@ -1930,8 +1958,13 @@ bool launch_pipe_g(const ContractArgs& p, hipStream_t s) {
     }
     return false;
   } else {
-    if (l1) contract_pipe<T, BN, 1, LA, LB, 0, false, G><<<p.total_tiles, 256, 0, s>>>(p);
-    else contract_pipe<T, BN, 2, LA, LB, 0, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+    if (p.vstore == 1 && !p.out_f32) {
+      if (l1) contract_pipe<T, BN, 1, LA, LB, 1, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+      else contract_pipe<T, BN, 2, LA, LB, 1, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+    } else {
+      if (l1) contract_pipe<T, BN, 1, LA, LB, 0, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+      else contract_pipe<T, BN, 2, LA, LB, 0, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+    }
     return true;
   }
 }
@@ -1951,12 +1984,8 @@ template <typename T, int BN, int LA, int LB>
 void launch_pipe(const ContractArgs& p, hipStream_t s) {
   if constexpr (LA == kKContig && LB == kKContig) {
     if (p.halo_n > 0) {
-      if constexpr (BN == 256) {
-        if (p.vstore == 1 && !p.out_f32) launch_pipe_halo<T, BN, 1>(p, s);
-        else launch_pipe_halo<T, BN, 0>(p, s);
-      } else {
-        launch_pipe_halo<T, BN, 0>(p, s);
-      }
+      if (p.vstore == 1 && !p.out_f32) launch_pipe_halo<T, BN, 1>(p, s);
+      else launch_pipe_halo<T, BN, 0>(p, s);
       return;
     }
   }
@@ -1970,14 +1999,14 @@ void launch_pipe(const ContractArgs& p, hipStream_t s) {
       }
       return;
     }
-    if (p.vstore == 1 && !p.out_f32) {
-      switch (p.klevels) {
-        case 1: contract_pipe<T, BN, 1, LA, LB, 1><<<p.total_tiles, 256, 0, s>>>(p); break;
-        case 2: contract_pipe<T, BN, 2, LA, LB, 1><<<p.total_tiles, 256, 0, s>>>(p); break;
-        default: contract_pipe<T, BN, kKLevels, LA, LB, 1><<<p.total_tiles, 256, 0, s>>>(p); break;
-      }
-      return;
+  }
+  if (p.vstore == 1 && !p.out_f32) {
+    switch (p.klevels) {
+      case 1: contract_pipe<T, BN, 1, LA, LB, 1><<<p.total_tiles, 256, 0, s>>>(p); break;
+      case 2: contract_pipe<T, BN, 2, LA, LB, 1><<<p.total_tiles, 256, 0, s>>>(p); break;
+      default: contract_pipe<T, BN, kKLevels, LA, LB, 1><<<p.total_tiles, 256, 0, s>>>(p); break;
     }
+    return;
   }
   switch (p.klevels) {
     case 1: contract_pipe<T, BN, 1, LA, LB><<<p.total_tiles, 256, 0, s>>>(p); break;
