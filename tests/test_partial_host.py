@@ -66,12 +66,57 @@ def test_distributed_einshard_requires_mesh():
         es.einshard_like("a b -> a/dp b", torch.randn(4, 3))
 
 
-def test_wrap_mesh_keeps_the_mesh(mesh_2d):
-    assert es.wrap_mesh(mesh_2d) is mesh_2d
+def test_wrap_mesh_gives_a_compound_mesh(mesh_2d):
+    # reference src/torch_einshard/mesh.py:15-70
     from torch_einshard.mesh_util import mesh_group_size
 
-    assert mesh_group_size(mesh_2d, "dp-sp") == 1
-    assert mesh_group_size(mesh_2d, "sp") == 1
+    wrapped = es.wrap_mesh(mesh_2d)
+    assert isinstance(wrapped, es.CompoundDeviceMesh)
+    assert es.wrap_mesh(wrapped) is wrapped
+    assert wrapped.mesh_dim_names == ("dp", "sp")
+    group = wrapped["dp-sp"].get_group()
+    assert torch.distributed.get_world_size(group) == 1
+    assert wrapped["sp-dp"].get_group() is group  # one group per set of dims
+    assert wrapped["dp"].size() == 1
+    for mesh in (wrapped, mesh_2d):
+        assert mesh_group_size(mesh, "dp-sp") == 1
+        assert mesh_group_size(mesh, "sp") == 1
+    with pytest.raises(ValueError, match="cannot contain empty mesh dimensions"):
+        wrapped["dp-"]
+    with pytest.raises(ValueError, match="cannot repeat mesh dimensions"):
+        wrapped["dp-dp"]
+
+
+class _Names:
+    """A mesh stand-in with the given dim names over a grid of matching rank."""
+
+    def __init__(self, names, rank=None):
+        self.mesh_dim_names = names
+        n = rank if rank is not None else (len(names) if isinstance(names, tuple) else 1)
+        self.mesh = torch.zeros((1,) * n, dtype=torch.int64)
+
+
+@pytest.mark.parametrize(
+    "names, error, message",
+    [
+        (("dp", 3), TypeError, "entries must be strings"),
+        (torch.zeros(2), TypeError, "must be an iterable of strings"),
+        (5, TypeError, "must be an iterable of strings"),
+        (("dp", ""), ValueError, "must be non-empty strings"),
+        (("dp-",), ValueError, "cannot contain empty compound components"),
+        (("dp-dp",), ValueError, "cannot repeat compound components"),
+        (("dp", "dp-sp"), ValueError, "cannot overlap compound components"),
+        (("dp", "dp"), ValueError, "cannot overlap compound components"),
+    ],
+)
+def test_compound_mesh_checks_dim_names(names, error, message):
+    with pytest.raises(error, match=message):
+        es.wrap_mesh(_Names(names, rank=2 if isinstance(names, tuple) and len(names) == 2 else 1))
+
+
+def test_compound_mesh_needs_one_name_per_dim():
+    with pytest.raises(ValueError, match="mesh_dim_names length must match mesh rank"):
+        es.wrap_mesh(_Names(("dp", "sp"), rank=3))
 
 
 class _Mesh:

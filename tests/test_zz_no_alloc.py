@@ -6,6 +6,8 @@ row, the second on a smaller input, so the second call also runs over scratch
 that still holds the first call's partials.  A descriptor needing more scratch
 than ES_NOALLOC_SCRATCH_BYTES would be refused with ES_ERR_WORKSPACE before any
 launch; no descriptor does (tests/test_abi.py checks the bound over a sweep).
+A call captured into a HIP graph (after an eager first call on the device) is
+replayed over new inputs and compared with es_reduce after every replay.
 """
 
 import ctypes
@@ -82,3 +84,38 @@ def test_noalloc_reduce_rejects_bad_descriptors_before_any_launch(gpu):
     desc = _middle_sum_desc(1, 8, 4, torch.float32)
     desc.n_red = 9
     assert lib.es_reduce_noalloc(ctypes.byref(desc), None, None, out.data_ptr(), None) == _native.ES_ERR_INVALID
+
+
+def test_noalloc_reduce_replays_from_a_captured_graph(gpu):
+    # the entry point's intended caller: a HIP graph.  The first call on the device
+    # (which looks up the scratch address) runs eagerly; the captured call is then
+    # replayed five times over new inputs written between the replays, each replay
+    # compared bit for bit with es_reduce on the same input.
+    lib = _native.lib()
+    b, n, h = 8, 2048, 1024
+    desc = _middle_sum_desc(b, n, h, torch.float32)
+    need = lib.es_reduce_workspace_bytes(ctypes.byref(desc))
+    assert 0 < need <= _native.NOALLOC_SCRATCH_BYTES
+    g = torch.Generator(device=gpu).manual_seed(9)
+    x = torch.rand(b, n, h, generator=g, device=gpu) * 2 - 1
+    out = torch.empty(b, h, device=gpu)
+    assert lib.es_reduce_noalloc(ctypes.byref(desc), x.data_ptr(), None, out.data_ptr(), _native.stream_of(x)) == 0
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream)
+        status = lib.es_reduce_noalloc(ctypes.byref(desc), x.data_ptr(), None, out.data_ptr(), stream)
+    assert status == 0, lib.es_last_error().decode()
+
+    want = torch.empty(b, h, device=gpu)
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    for replay in range(5):
+        x.copy_(torch.rand(b, n, h, generator=g, device=gpu) * 2 - 1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        stream = _native.stream_of(x)
+        assert lib.es_reduce(ctypes.byref(desc), x.data_ptr(), None, want.data_ptr(), ws.data_ptr(), need, stream) == 0
+        torch.cuda.synchronize()
+        assert_bitexact(out, want)

@@ -4,12 +4,12 @@ Public surface kept from the reference (src/torch_einshard/__init__.py:1-57,
 346-372): ``einshard``, ``einshard_like``, ``einwindow``, ``einhalo``, the
 notation types, ``PlanPolicy`` / ``optimize`` and the plan diagnostics, and
 ``einconv`` (src/torch_einshard/conv.py:65) and ``einroll``
-(src/torch_einshard/roll.py:10).
+(src/torch_einshard/roll.py:10); ``helpers`` keeps the reference's split-shape helpers.
 Arithmetic runs on hand-written HIP kernels (libeinshard_hip.so) on ROCm
 device tensors; there is no CPU path and no fallback to ``torch.einsum``.
 """
 
-from . import symbolic
+from . import helpers, symbolic
 from ._cache import call_key, lookup, remember
 from ._exec import launch
 from .autograd import needs_grad
@@ -19,7 +19,7 @@ from .einsum import einsum, equation_of, prepare_local
 from .families import cached_expand_axis_families
 from .grammar import Axes, parse_sharding
 from .halo import einhalo, einwindow
-from .mesh_util import wrap_mesh
+from .mesh_util import CompoundDeviceMesh, wrap_mesh
 from .roll import einroll
 from .sharding import Axis, AxisGroup, EllipsisAxis, TensorAnnotation, TensorSpec
 from .symbolic import (
@@ -44,6 +44,7 @@ __all__ = [
     "einconv",
     "einroll",
     "wrap_mesh",
+    "CompoundDeviceMesh",
     "einsum",
     "equation_of",
     "parse_sharding",

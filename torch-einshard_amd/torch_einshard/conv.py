@@ -461,7 +461,7 @@ def einconv(
 
     def pad_plan(x_arg):
         # halo + permutation to (batch..., spatial..., channel) in one gather
-        _check_padding(x_arg, input_axes, halos, mesh=mesh, boundary=boundary)
+        _check_padding(x_arg, input_axes, halos, mesh=mesh, boundary=boundary, shapes=shapes)
         if x_arg.dim() != len(input_axes):
             raise ValueError(f"einconv: spec has {len(input_axes)} axes but the input has {x_arg.dim()} dims")
         canon = batch + spatial + [channel]

@@ -16,7 +16,6 @@ policy context, :392-445 for ``ExecutionPlan`` / ``last_plan``):
 from contextlib import contextmanager
 from contextvars import ContextVar
 from dataclasses import dataclass
-from typing import NamedTuple
 
 __all__ = [
     "PlanPolicy",
@@ -149,9 +148,12 @@ class PlanStep:
     args: tuple = ()
 
 
-class PlanCandidate(NamedTuple):
+@dataclass(frozen=True)
+class PlanCandidate:
     """A strategy an operation weighed, and what became of it (``status``:
-    considered / accepted / rejected / ranked / selected, with a ``reason``)."""
+    considered / accepted / rejected / ranked / selected, with a ``reason``).  A frozen
+    dataclass with the reference's fields (symbolic.py:147-156): callers compare,
+    hash and inspect candidates with ``dataclasses`` as they do there."""
 
     name: str
     args: tuple = ()
@@ -160,15 +162,14 @@ class PlanCandidate(NamedTuple):
     reason: str = ""
 
     def with_result(self, status, reason=""):
-        return self._replace(status=status, reason=reason)
+        """The same candidate with a new status and reason."""
+        return PlanCandidate(self.name, self.args, self.fallback_steps, status, reason)
 
 
 class ExecutionPlan:
     """The record of one operation: the steps it ran, in order, plus the
     candidates it weighed and the alternatives it ranked.  Method names and
     arguments are the reference's (symbolic.py:392-421)."""
-
-    __slots__ = ("steps", "candidates", "alternatives")
 
     def __init__(self):
         self.steps, self.candidates, self.alternatives = [], [], []
