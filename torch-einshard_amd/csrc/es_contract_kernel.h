@@ -1473,7 +1473,13 @@ __device__ __forceinline__ void store_pipe_f32(const ContractArgs& p, typename T
 // halo): every row, column and batch offset is an unrolled walk of G - 1 divisions, so the
 // set-up in front of the first copies is a few hundred instructions instead of a walk over
 // ES_MAX_AXES sub-axes per row with a scalar load per step.
-template <typename T, int BN, int L, int LA, int LB, int EPI = 0, bool HALO = false, int G = 0>
+// A3 (K-contiguous operands, no halo, 224-wide tiles): A, the operand each tile streams
+// from its own rows, gets three LDS stages and B two, so A's copies run two K tiles ahead
+// (B's one): in step kt the copies of B tile kt+2 and A tile kt+3 go into the stages
+// that step kt's first substep finished reading, B's first, and the barrier waits for all
+// but the last A tile's copies (loads complete in order).  On a cold cache a copy from
+// HBM takes longer than one K step; with one tile of lead the loop waited for it.
+template <typename T, int BN, int L, int LA, int LB, int EPI = 0, bool HALO = false, int G = 0, bool A3 = false>
 __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   using S = typename Traits<T>::S;
   constexpr int BM = 256, WM = 2, WN = 2;
@@ -1489,6 +1495,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
       std::conditional_t<LA == kMNContig, PipeCopiesMN<S, BM, WM * WN, 0, G>, PipeCopies<S, BM, WM * WN, 0, G>>>;
   static_assert(!HALO || (LA == kKContig && LB == kKContig), "the halo reads K-contiguous operands");
   static_assert(G == 0 || !HALO, "the halo copies walk the M group themselves");
+  static_assert(!A3 || (!HALO && LA == kKContig && LB == kKContig && BN == 224), "three A stages of 224-wide tiles");
   using CopyB =
       std::conditional_t<LB == kMNContig, PipeCopiesMN<S, BN, WM * WN, 1, G>, PipeCopies<S, BN, WM * WN, 1, G>>;
   using FragA = PipeFrag<S, LA>;
@@ -1502,8 +1509,14 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
 
   // EPI 1 stages 128 rows of 256 elements per stage (more than a 224-wide tile's K stage)
   constexpr int STAGE_ALLOC = EPI == 1 && STAGE < 128 * 256 ? 128 * 256 : STAGE;
-  __shared__ __attribute__((aligned(1024))) S lds0[STAGE_ALLOC];
-  __shared__ __attribute__((aligned(1024))) S lds1[STAGE_ALLOC];
+  // A3: one ring of three A stages then two B stages; the epilogue stages its two halves at
+  // its start and 64 KB in
+  constexpr int A_TILE = BM * BK, B_TILE = BN * BK;
+  constexpr int RING = 3 * A_TILE + 2 * B_TILE;
+  static_assert(!A3 || RING >= 2 * 128 * 256, "the epilogue's two halves fit the ring");
+  __shared__ __attribute__((aligned(1024))) S lds0[A3 ? RING : STAGE_ALLOC];
+  __shared__ __attribute__((aligned(1024))) S lds1_own[A3 ? 1 : STAGE_ALLOC];
+  S* const lds1 = A3 ? lds0 + 128 * 256 : lds1_own;
   // the one-pass epilogue's row and column offset tables
   __shared__ int64_t ep_tables[EPI == 1 ? BM + 256 : 1];
   // EPI 1 with bounded groups forms those tables in the prologue (while the first copies
@@ -1580,6 +1593,113 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
       cb.issue_one(q - CopyA::NI, static_cast<const S*>(p.b) + w.ob, stage + uint32_t(BM * BK * sizeof(S)));
     }
   };
+  // the epilogue's output pointer and bias test (see kPreTables)
+  S* out_c;
+  uint32_t has_bias;
+  if constexpr (A3) {
+    // the ring's stages: A stage i at lds0 + i * A_TILE, B stage j after the three A stages
+    const uint32_t ring_addr = lds_address(lds0);
+    auto a_stage = [&](uint32_t i) { return lds0 + i * A_TILE; };
+    auto b_stage = [&](uint32_t j) { return lds0 + 3 * A_TILE + j * B_TILE; };
+    PipeWalk<L> wa;  // the next A tile to copy
+    wa.start(p);
+    auto copy_a = [&](int q, uint32_t i) {
+      ca.issue_one(q, static_cast<const S*>(p.a) + wa.oa, ring_addr + i * uint32_t(A_TILE * sizeof(S)));
+    };
+    auto copy_b = [&](int q, uint32_t j) {
+      cb.issue_one(q, static_cast<const S*>(p.b) + w.ob, ring_addr + uint32_t((3 * A_TILE + j * B_TILE) * sizeof(S)));
+    };
+    // K tiles 0 and 1 of both operands and A's tile 2, in the order the barriers count them:
+    // A0 B0 | B1 A1 | A2
+#pragma unroll
+    for (int q = 0; q < CopyA::NI; ++q) copy_a(q, 0);
+#pragma unroll
+    for (int q = 0; q < CopyB::NI; ++q) copy_b(q, 0);
+    wa.advance(nk);
+    w.advance(nk);
+#pragma unroll
+    for (int q = 0; q < CopyB::NI; ++q) copy_b(q, 1);
+#pragma unroll
+    for (int q = 0; q < CopyA::NI; ++q) copy_a(q, 1);
+    wa.advance(nk);
+    w.advance(nk);
+#pragma unroll
+    for (int q = 0; q < CopyA::NI; ++q) copy_a(q, 2);
+    wa.advance(nk);
+  out_c = static_cast<S*>(p.c);
+  has_bias = p.bias != nullptr ? 1u : 0u;
+  if constexpr (kPreTables) {
+    const uint32_t m = m0 + tid, n = n0 + tid;
+    ep_tables[tid] = m < p.M ? boff_c + group_offset_d<2, G>(p.gm, m) : -1;
+    if (tid < BN) ep_tables[BM + tid] = n < p.N ? group_offset_d<2, G>(p.gn, n) : -1;
+    const uint64_t cbits = reinterpret_cast<uint64_t>(out_c);
+    uint32_t clo = __builtin_amdgcn_readfirstlane(uint32_t(cbits));
+    uint32_t chi = __builtin_amdgcn_readfirstlane(uint32_t(cbits >> 32));
+    has_bias = __builtin_amdgcn_readfirstlane(has_bias);
+    asm volatile("" : "+s"(clo), "+s"(chi), "+s"(has_bias));
+    out_c = reinterpret_cast<S*>((uint64_t(chi) << 32) | clo);
+  }
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY + CopyA::NI) : "memory");  // K tile 0 landed
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[0][i] = fa.read(a_stage(0), i, 0);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[0][j] = fb.read(b_stage(0), j, 0);
+    // step kt: a_cur = kt % 3, b_cur = kt % 2
+    auto step3 = [&](uint32_t a_cur, uint32_t a_nxt, uint32_t b_cur, uint32_t b_nxt, auto first) {
+      const S* as = a_stage(a_cur);
+      const S* bs = b_stage(b_cur);
+#pragma unroll
+      for (int q = 0; q < MMAS; ++q) {
+        if constexpr (decltype(first)::value) PipeMma<T>::mma_first(acc[q / FN][q % FN], bf[0][q % FN], af[0][q / FN]);
+        else PipeMma<T>::mma(acc[q / FN][q % FN], bf[0][q % FN], af[0][q / FN]);
+        const int r0 = (q * (FM + FN)) / MMAS, r1 = ((q + 1) * (FM + FN)) / MMAS;
+        if (r0 != r1) {
+          if (r0 < FM) af[1][r0] = fa.read(as, r0, 1);
+          else bf[1][r0 - FM] = fb.read(bs, r0 - FM, 1);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // K tile kt+1 of both operands landed (the copies still allowed in flight are A's
+      // last batch, tile kt+2); every read of stages a_cur and b_cur done
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CopyA::NI) : "memory");
+      __syncthreads();
+      const S* an = a_stage(a_nxt);
+      const S* bn = b_stage(b_nxt);
+#pragma unroll
+      for (int q = 0; q < MMAS; ++q) {
+        PipeMma<T>::mma(acc[q / FN][q % FN], bf[1][q % FN], af[1][q / FN]);
+        // B tile kt+2 into b_cur, then A tile kt+3 into a_cur
+        const int c0 = (q * NCOPY) / MMAS, c1 = ((q + 1) * NCOPY) / MMAS;
+        if (c0 != c1) {
+          if (c0 < CopyB::NI) copy_b(c0, b_cur);
+          else copy_a(c0 - CopyB::NI, a_cur);
+        }
+        const int r0 = (q * (FM + FN)) / MMAS, r1 = ((q + 1) * (FM + FN)) / MMAS;
+        if (r0 != r1) {
+          if (r0 < FM) af[0][r0] = fa.read(an, r0, 0);
+          else bf[0][r0 - FM] = fb.read(bn, r0 - FM, 0);
+        }
+      }
+      w.advance(nk);
+      wa.advance(nk);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    using First = std::integral_constant<bool, true>;
+    using Next = std::integral_constant<bool, false>;
+    // the stages repeat every 6 K tiles
+    step3(0, 1, 0, 1, First{});
+    uint32_t kt = 1;
+    for (; kt + 5 < nk; kt += 6) {
+      step3(1, 2, 1, 0, Next{});
+      step3(2, 0, 0, 1, Next{});
+      step3(0, 1, 1, 0, Next{});
+      step3(1, 2, 0, 1, Next{});
+      step3(2, 0, 1, 0, Next{});
+      step3(0, 1, 0, 1, Next{});
+    }
+    for (; kt < nk; ++kt) step3(kt % 3, (kt + 1) % 3, kt % 2, (kt + 1) % 2, Next{});
+  } else {
   halo_voffs();
 #pragma unroll
   for (int q = 0; q < NCOPY; ++q) copy(q, lds0_addr);
@@ -1588,8 +1708,8 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
 #pragma unroll
   for (int q = 0; q < NCOPY; ++q) copy(q, lds1_addr);
   w.advance(nk);
-  S* out_c = static_cast<S*>(p.c);
-  uint32_t has_bias = p.bias != nullptr ? 1u : 0u;
+  out_c = static_cast<S*>(p.c);
+  has_bias = p.bias != nullptr ? 1u : 0u;
   if constexpr (kPreTables) {
     const uint32_t m = m0 + tid, n = n0 + tid;
     ep_tables[tid] = m < p.M ? boff_c + group_offset_d<2, G>(p.gm, m) : -1;
@@ -1653,6 +1773,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
     step(lds0, lds1, lds0_addr, Next{});
   }
   if (kt < nk) step(lds1, lds0, lds1_addr, Next{});
+  }
   pipe_drain(acc);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -1958,12 +2079,14 @@ bool launch_pipe_g(const ContractArgs& p, hipStream_t s) {
     }
     return false;
   } else {
+    // 224-wide tiles with both operands K-contiguous give A a third LDS stage (A3)
+    constexpr bool A3 = LA == kKContig && LB == kKContig;
     if (p.vstore == 1 && !p.out_f32) {
-      if (l1) contract_pipe<T, BN, 1, LA, LB, 1, false, G><<<p.total_tiles, 256, 0, s>>>(p);
-      else contract_pipe<T, BN, 2, LA, LB, 1, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+      if (l1) contract_pipe<T, BN, 1, LA, LB, 1, false, G, A3><<<p.total_tiles, 256, 0, s>>>(p);
+      else contract_pipe<T, BN, 2, LA, LB, 1, false, G, A3><<<p.total_tiles, 256, 0, s>>>(p);
     } else {
-      if (l1) contract_pipe<T, BN, 1, LA, LB, 0, false, G><<<p.total_tiles, 256, 0, s>>>(p);
-      else contract_pipe<T, BN, 2, LA, LB, 0, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+      if (l1) contract_pipe<T, BN, 1, LA, LB, 0, false, G, A3><<<p.total_tiles, 256, 0, s>>>(p);
+      else contract_pipe<T, BN, 2, LA, LB, 0, false, G, A3><<<p.total_tiles, 256, 0, s>>>(p);
     }
     return true;
   }
