@@ -141,7 +141,9 @@ int es_reduce(const es_reduce_desc* desc, const void* x, const void* y, void* ou
  * ES_ERR_WORKSPACE before any launch.  The scratch needs no clearing (every partial
  * is written before it is read), keeps the last call's contents, and is shared by
  * every call on that GPU: calls that overlap on one GPU (other streams, other
- * threads) race on it. */
+ * threads, graph replays in flight together) race on it.  The first call on a device
+ * looks up the array's address there; make it outside any graph capture.  A captured
+ * call replays like any launch. */
 #define ES_NOALLOC_SCRATCH_BYTES (8 * 1024 * 1024)
 int es_reduce_noalloc(const es_reduce_desc* desc, const void* x, const void* y, void* out, void* stream);
 
