@@ -93,6 +93,7 @@ struct Traits<f16_t> {
 // rows, one chunk) and the global->LDS writes are free of bank conflicts.
 constexpr int kRowBytes = 128;
 constexpr int kChunks = kRowBytes / 16;  // 8
+constexpr int kLdsBytes = 160 * 1024;    // LDS of one work-group on gfx950
 
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & (kChunks - 1)); }
 
@@ -1473,13 +1474,17 @@ __device__ __forceinline__ void store_pipe_f32(const ContractArgs& p, typename T
 // halo): every row, column and batch offset is an unrolled walk of G - 1 divisions, so the
 // set-up in front of the first copies is a few hundred instructions instead of a walk over
 // ES_MAX_AXES sub-axes per row with a scalar load per step.
-// A3 (K-contiguous operands, no halo, 224-wide tiles): A, the operand each tile streams
-// from its own rows, gets three LDS stages and B two, so A's copies run two K tiles ahead
-// (B's one): in step kt the copies of B tile kt+2 and A tile kt+3 go into the stages
-// that step kt's first substep finished reading, B's first, and the barrier waits for all
-// but the last A tile's copies (loads complete in order).  On a cold cache a copy from
-// HBM takes longer than one K step; with one tile of lead the loop waited for it.
-template <typename T, int BN, int L, int LA, int LB, int EPI = 0, bool HALO = false, int G = 0, bool A3 = false>
+// X3 (no halo): one operand, the deep one (1: A, 2: B), gets three LDS stages and the
+// other two, so the deep operand's copies run two K tiles ahead (the other's one): in
+// step kt the copies of the other's tile kt+2 and the deep operand's tile kt+3 go into
+// the stages that step kt's first substep finished reading, the other's first, and the
+// barrier waits for all but the deep operand's last batch (loads complete in order).  On
+// a cold cache a copy from HBM takes longer than one K step; with one tile of lead the
+// loop waited for it.  The deep operand is the one with more rows of its own to stream
+// (A for 16384 x 1792, B for 2048 x 8192).  224-wide tiles: A, with both operands
+// K-contiguous.  256-wide tiles (EPI 1): the ring takes all 160 KB of LDS, so the
+// epilogue's offset tables wait in registers through the K loop and go to LDS after it.
+template <typename T, int BN, int L, int LA, int LB, int EPI = 0, bool HALO = false, int G = 0, int X3 = 0>
 __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   using S = typename Traits<T>::S;
   constexpr int BM = 256, WM = 2, WN = 2;
@@ -1495,7 +1500,8 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
       std::conditional_t<LA == kMNContig, PipeCopiesMN<S, BM, WM * WN, 0, G>, PipeCopies<S, BM, WM * WN, 0, G>>>;
   static_assert(!HALO || (LA == kKContig && LB == kKContig), "the halo reads K-contiguous operands");
   static_assert(G == 0 || !HALO, "the halo copies walk the M group themselves");
-  static_assert(!A3 || (!HALO && LA == kKContig && LB == kKContig && BN == 224), "three A stages of 224-wide tiles");
+  static_assert(X3 == 0 || (!HALO && (BN == 224 ? X3 == 1 && LA == kKContig && LB == kKContig : EPI == 1 && G > 0)),
+                "three stages: A of 224-wide K-contiguous tiles, or either of 256-wide tiles with EPI 1 and bounded groups");
   using CopyB =
       std::conditional_t<LB == kMNContig, PipeCopiesMN<S, BN, WM * WN, 1, G>, PipeCopies<S, BN, WM * WN, 1, G>>;
   using FragA = PipeFrag<S, LA>;
@@ -1509,20 +1515,30 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
 
   // EPI 1 stages 128 rows of 256 elements per stage (more than a 224-wide tile's K stage)
   constexpr int STAGE_ALLOC = EPI == 1 && STAGE < 128 * 256 ? 128 * 256 : STAGE;
-  // A3: one ring of three A stages then two B stages; the epilogue stages its two halves at
+  // X3: one ring of the A stages then the B stages; the epilogue stages its two halves at
   // its start and 64 KB in
   constexpr int A_TILE = BM * BK, B_TILE = BN * BK;
-  constexpr int RING = 3 * A_TILE + 2 * B_TILE;
-  static_assert(!A3 || RING >= 2 * 128 * 256, "the epilogue's two halves fit the ring");
-  __shared__ __attribute__((aligned(1024))) S lds0[A3 ? RING : STAGE_ALLOC];
-  __shared__ __attribute__((aligned(1024))) S lds1_own[A3 ? 1 : STAGE_ALLOC];
-  S* const lds1 = A3 ? lds0 + 128 * 256 : lds1_own;
-  // the one-pass epilogue's row and column offset tables
-  __shared__ int64_t ep_tables[EPI == 1 ? BM + 256 : 1];
+  constexpr int NA = X3 == 1 ? 3 : 2, NB = X3 == 2 ? 3 : 2;  // stages of A and of B
+  constexpr int RING = NA * A_TILE + NB * B_TILE;
+  static_assert(X3 == 0 || RING >= 2 * 128 * 256, "the epilogue's two halves fit the ring");
+  constexpr int STAGES_BYTES = (X3 ? RING : 2 * STAGE_ALLOC) * int(sizeof(S));
+  // the one-pass epilogue's row and column offset tables: LDS of their own when that fits
+  // beside the stages, else (a 256-wide ring) the ring's bytes past the staged halves
+  constexpr int TABLE_BYTES = (BM + 256) * int(sizeof(int64_t));
+  constexpr bool kOwnTables = EPI == 1 && STAGES_BYTES + TABLE_BYTES <= kLdsBytes;
+  static_assert(EPI != 1 || kOwnTables || 2 * 128 * 256 * int(sizeof(S)) + TABLE_BYTES <= STAGES_BYTES, "tables fit");
+  __shared__ __attribute__((aligned(1024))) char lds_raw[STAGES_BYTES + (kOwnTables ? TABLE_BYTES : 0)];
+  S* const lds0 = reinterpret_cast<S*>(lds_raw);
+  S* const lds1 = lds0 + (X3 ? 128 * 256 : STAGE_ALLOC);
+  int64_t* const ep_tables =
+      reinterpret_cast<int64_t*>(lds_raw + (kOwnTables ? STAGES_BYTES : 2 * 128 * 256 * int(sizeof(S))));
   // EPI 1 with bounded groups forms those tables in the prologue (while the first copies
-  // are in flight) and keeps the output pointer and the bias test in scalar registers
-  // through the K loop: the epilogue then reads no kernel argument
+  // are in flight: into LDS, or with no LDS of their own into registers, one row and one
+  // column offset per thread, stored after the K loop) and keeps the output pointer and
+  // the bias test in scalar registers through the K loop: the epilogue then reads no
+  // kernel argument
   constexpr bool kPreTables = EPI == 1 && G > 0;
+  int64_t reg_row = -1, reg_col = -1;
 
   const int tid = threadIdx.x;
   const int lane = tid % 64;
@@ -1596,59 +1612,79 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   // the epilogue's output pointer and bias test (see kPreTables)
   S* out_c;
   uint32_t has_bias;
-  if constexpr (A3) {
-    // the ring's stages: A stage i at lds0 + i * A_TILE, B stage j after the three A stages
+  auto pre_tables = [&]() {
+    out_c = static_cast<S*>(p.c);
+    has_bias = p.bias != nullptr ? 1u : 0u;
+    if constexpr (kPreTables) {
+      const uint32_t m = m0 + tid, n = n0 + tid;
+      reg_row = m < p.M ? boff_c + group_offset_d<2, G>(p.gm, m) : -1;
+      reg_col = tid < BN && n < p.N ? group_offset_d<2, G>(p.gn, n) : -1;
+      if constexpr (kOwnTables) {
+        ep_tables[tid] = reg_row;
+        if (tid < BN) ep_tables[BM + tid] = reg_col;
+      }
+      const uint64_t cbits = reinterpret_cast<uint64_t>(out_c);
+      uint32_t clo = __builtin_amdgcn_readfirstlane(uint32_t(cbits));
+      uint32_t chi = __builtin_amdgcn_readfirstlane(uint32_t(cbits >> 32));
+      has_bias = __builtin_amdgcn_readfirstlane(has_bias);
+      asm volatile("" : "+s"(clo), "+s"(chi), "+s"(has_bias));
+      out_c = reinterpret_cast<S*>((uint64_t(chi) << 32) | clo);
+    }
+  };
+  if constexpr (X3 != 0) {
+    // the ring's stages: A stage i at lds0 + i * A_TILE, B stage j after the NA A stages
     const uint32_t ring_addr = lds_address(lds0);
     auto a_stage = [&](uint32_t i) { return lds0 + i * A_TILE; };
-    auto b_stage = [&](uint32_t j) { return lds0 + 3 * A_TILE + j * B_TILE; };
-    PipeWalk<L> wa;  // the next A tile to copy
-    wa.start(p);
-    auto copy_a = [&](int q, uint32_t i) {
-      ca.issue_one(q, static_cast<const S*>(p.a) + wa.oa, ring_addr + i * uint32_t(A_TILE * sizeof(S)));
+    auto b_stage = [&](uint32_t j) { return lds0 + NA * A_TILE + j * B_TILE; };
+    PipeWalk<L> wd;  // the deep operand's next K tile to copy
+    wd.start(p);
+    // the other operand's next K tile (from step 0 on) is the one before the deep
+    // operand's: its offset is the walk's, kept from before the walk's last advance
+    auto other_off = [&]() { return X3 == 1 ? wd.ob : wd.oa; };
+    int64_t o_off = 0;
+    constexpr int NI_D = X3 == 1 ? CopyA::NI : CopyB::NI;  // copies per K tile: deep operand
+    constexpr int NI_O = NCOPY - NI_D;                      // ... and the other
+    // copy q of the deep (other) operand's next K tile into its stage `st`
+    auto copy_d = [&](int q, uint32_t st) {
+      if constexpr (X3 == 1)
+        ca.issue_one(q, static_cast<const S*>(p.a) + wd.oa, ring_addr + st * uint32_t(A_TILE * sizeof(S)));
+      else
+        cb.issue_one(q, static_cast<const S*>(p.b) + wd.ob,
+                     ring_addr + uint32_t((NA * A_TILE + st * B_TILE) * sizeof(S)));
     };
-    auto copy_b = [&](int q, uint32_t j) {
-      cb.issue_one(q, static_cast<const S*>(p.b) + w.ob, ring_addr + uint32_t((3 * A_TILE + j * B_TILE) * sizeof(S)));
+    auto copy_o = [&](int q, uint32_t st, int64_t off) {
+      if constexpr (X3 == 1)
+        cb.issue_one(q, static_cast<const S*>(p.b) + off, ring_addr + uint32_t((NA * A_TILE + st * B_TILE) * sizeof(S)));
+      else
+        ca.issue_one(q, static_cast<const S*>(p.a) + off, ring_addr + st * uint32_t(A_TILE * sizeof(S)));
     };
-    // K tiles 0 and 1 of both operands and A's tile 2, in the order the barriers count them:
-    // A0 B0 | B1 A1 | A2
+    // K tiles 0 and 1 of both operands and the deep operand's tile 2, in the order the
+    // barriers count them: D0 O0 | O1 D1 | D2
 #pragma unroll
-    for (int q = 0; q < CopyA::NI; ++q) copy_a(q, 0);
+    for (int q = 0; q < NI_D; ++q) copy_d(q, 0);
 #pragma unroll
-    for (int q = 0; q < CopyB::NI; ++q) copy_b(q, 0);
-    wa.advance(nk);
-    w.advance(nk);
+    for (int q = 0; q < NI_O; ++q) copy_o(q, 0, other_off());
+    wd.advance(nk);
 #pragma unroll
-    for (int q = 0; q < CopyB::NI; ++q) copy_b(q, 1);
+    for (int q = 0; q < NI_O; ++q) copy_o(q, 1, other_off());
 #pragma unroll
-    for (int q = 0; q < CopyA::NI; ++q) copy_a(q, 1);
-    wa.advance(nk);
-    w.advance(nk);
+    for (int q = 0; q < NI_D; ++q) copy_d(q, 1);
+    wd.advance(nk);
 #pragma unroll
-    for (int q = 0; q < CopyA::NI; ++q) copy_a(q, 2);
-    wa.advance(nk);
-  out_c = static_cast<S*>(p.c);
-  has_bias = p.bias != nullptr ? 1u : 0u;
-  if constexpr (kPreTables) {
-    const uint32_t m = m0 + tid, n = n0 + tid;
-    ep_tables[tid] = m < p.M ? boff_c + group_offset_d<2, G>(p.gm, m) : -1;
-    if (tid < BN) ep_tables[BM + tid] = n < p.N ? group_offset_d<2, G>(p.gn, n) : -1;
-    const uint64_t cbits = reinterpret_cast<uint64_t>(out_c);
-    uint32_t clo = __builtin_amdgcn_readfirstlane(uint32_t(cbits));
-    uint32_t chi = __builtin_amdgcn_readfirstlane(uint32_t(cbits >> 32));
-    has_bias = __builtin_amdgcn_readfirstlane(has_bias);
-    asm volatile("" : "+s"(clo), "+s"(chi), "+s"(has_bias));
-    out_c = reinterpret_cast<S*>((uint64_t(chi) << 32) | clo);
-  }
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY + CopyA::NI) : "memory");  // K tile 0 landed
+    for (int q = 0; q < NI_D; ++q) copy_d(q, 2);
+    o_off = other_off();
+    wd.advance(nk);
+    pre_tables();
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY + NI_D) : "memory");  // K tile 0 landed
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < FM; ++i) af[0][i] = fa.read(a_stage(0), i, 0);
 #pragma unroll
     for (int j = 0; j < FN; ++j) bf[0][j] = fb.read(b_stage(0), j, 0);
-    // step kt: a_cur = kt % 3, b_cur = kt % 2
-    auto step3 = [&](uint32_t a_cur, uint32_t a_nxt, uint32_t b_cur, uint32_t b_nxt, auto first) {
-      const S* as = a_stage(a_cur);
-      const S* bs = b_stage(b_cur);
+    // step kt: the deep operand's stage d_cur = kt % 3, the other's o_cur = kt % 2
+    auto step3 = [&](uint32_t d_cur, uint32_t d_nxt, uint32_t o_cur, uint32_t o_nxt, auto first) {
+      const S* as = a_stage(X3 == 1 ? d_cur : o_cur);
+      const S* bs = b_stage(X3 == 1 ? o_cur : d_cur);
 #pragma unroll
       for (int q = 0; q < MMAS; ++q) {
         if constexpr (decltype(first)::value) PipeMma<T>::mma_first(acc[q / FN][q % FN], bf[0][q % FN], af[0][q / FN]);
@@ -1660,20 +1696,20 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      // K tile kt+1 of both operands landed (the copies still allowed in flight are A's
-      // last batch, tile kt+2); every read of stages a_cur and b_cur done
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CopyA::NI) : "memory");
+      // K tile kt+1 of both operands landed (the copies still allowed in flight are the
+      // deep operand's last batch, tile kt+2); every read of the current stages done
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NI_D) : "memory");
       __syncthreads();
-      const S* an = a_stage(a_nxt);
-      const S* bn = b_stage(b_nxt);
+      const S* an = a_stage(X3 == 1 ? d_nxt : o_nxt);
+      const S* bn = b_stage(X3 == 1 ? o_nxt : d_nxt);
 #pragma unroll
       for (int q = 0; q < MMAS; ++q) {
         PipeMma<T>::mma(acc[q / FN][q % FN], bf[1][q % FN], af[1][q / FN]);
-        // B tile kt+2 into b_cur, then A tile kt+3 into a_cur
+        // the other operand's tile kt+2 into o_cur, then the deep operand's kt+3 into d_cur
         const int c0 = (q * NCOPY) / MMAS, c1 = ((q + 1) * NCOPY) / MMAS;
         if (c0 != c1) {
-          if (c0 < CopyB::NI) copy_b(c0, b_cur);
-          else copy_a(c0 - CopyB::NI, a_cur);
+          if (c0 < NI_O) copy_o(c0, o_cur, o_off);
+          else copy_d(c0 - NI_O, d_cur);
         }
         const int r0 = (q * (FM + FN)) / MMAS, r1 = ((q + 1) * (FM + FN)) / MMAS;
         if (r0 != r1) {
@@ -1681,8 +1717,8 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
           else bf[0][r0 - FM] = fb.read(bn, r0 - FM, 0);
         }
       }
-      w.advance(nk);
-      wa.advance(nk);
+      o_off = other_off();
+      wd.advance(nk);
       __builtin_amdgcn_sched_barrier(0);
     };
     using First = std::integral_constant<bool, true>;
@@ -1708,19 +1744,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
 #pragma unroll
   for (int q = 0; q < NCOPY; ++q) copy(q, lds1_addr);
   w.advance(nk);
-  out_c = static_cast<S*>(p.c);
-  has_bias = p.bias != nullptr ? 1u : 0u;
-  if constexpr (kPreTables) {
-    const uint32_t m = m0 + tid, n = n0 + tid;
-    ep_tables[tid] = m < p.M ? boff_c + group_offset_d<2, G>(p.gm, m) : -1;
-    if (tid < BN) ep_tables[BM + tid] = n < p.N ? group_offset_d<2, G>(p.gn, n) : -1;
-    const uint64_t cbits = reinterpret_cast<uint64_t>(out_c);
-    uint32_t clo = __builtin_amdgcn_readfirstlane(uint32_t(cbits));
-    uint32_t chi = __builtin_amdgcn_readfirstlane(uint32_t(cbits >> 32));
-    has_bias = __builtin_amdgcn_readfirstlane(has_bias);
-    asm volatile("" : "+s"(clo), "+s"(chi), "+s"(has_bias));
-    out_c = reinterpret_cast<S*>((uint64_t(chi) << 32) | clo);
-  }
+  pre_tables();
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY) : "memory");  // K tile 0 of this wave landed
   __syncthreads();
   frags(lds0, 0, 0);
@@ -1778,6 +1802,10 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if constexpr (EPI == 1) {
+    if constexpr (kPreTables && !kOwnTables) {
+      ep_tables[tid] = reg_row;  // the ring is free: every wave passed the barrier above
+      if (tid < BN) ep_tables[BM + tid] = reg_col;
+    }
     if (has_bias)
       store_pipe_wide<T, BN, FM, FN, true, G, kPreTables>(p, lds0, lds1, acc, m0, n0, boff_c, ep_tables, out_c);
     else
@@ -2073,20 +2101,26 @@ bool launch_pipe_g(const ContractArgs& p, hipStream_t s) {
       return true;
     }
     if (p.vstore == 1 && !p.out_f32) {
-      if (l1) contract_pipe<T, BN, 1, LA, LB, 1, false, G><<<p.total_tiles, 256, 0, s>>>(p);
-      else contract_pipe<T, BN, 2, LA, LB, 1, false, G><<<p.total_tiles, 256, 0, s>>>(p);
+      // the operand with more rows to stream takes a third LDS stage (X3 = 2: B, 1: A)
+      if (p.N > p.M) {
+        if (l1) contract_pipe<T, BN, 1, LA, LB, 1, false, G, 2><<<p.total_tiles, 256, 0, s>>>(p);
+        else contract_pipe<T, BN, 2, LA, LB, 1, false, G, 2><<<p.total_tiles, 256, 0, s>>>(p);
+      } else {
+        if (l1) contract_pipe<T, BN, 1, LA, LB, 1, false, G, 1><<<p.total_tiles, 256, 0, s>>>(p);
+        else contract_pipe<T, BN, 2, LA, LB, 1, false, G, 1><<<p.total_tiles, 256, 0, s>>>(p);
+      }
       return true;
     }
     return false;
   } else {
-    // 224-wide tiles with both operands K-contiguous give A a third LDS stage (A3)
-    constexpr bool A3 = LA == kKContig && LB == kKContig;
+    // 224-wide tiles with both operands K-contiguous give A a third LDS stage (X3 = 1)
+    constexpr int X3 = LA == kKContig && LB == kKContig ? 1 : 0;
     if (p.vstore == 1 && !p.out_f32) {
-      if (l1) contract_pipe<T, BN, 1, LA, LB, 1, false, G, A3><<<p.total_tiles, 256, 0, s>>>(p);
-      else contract_pipe<T, BN, 2, LA, LB, 1, false, G, A3><<<p.total_tiles, 256, 0, s>>>(p);
+      if (l1) contract_pipe<T, BN, 1, LA, LB, 1, false, G, X3><<<p.total_tiles, 256, 0, s>>>(p);
+      else contract_pipe<T, BN, 2, LA, LB, 1, false, G, X3><<<p.total_tiles, 256, 0, s>>>(p);
     } else {
-      if (l1) contract_pipe<T, BN, 1, LA, LB, 0, false, G, A3><<<p.total_tiles, 256, 0, s>>>(p);
-      else contract_pipe<T, BN, 2, LA, LB, 0, false, G, A3><<<p.total_tiles, 256, 0, s>>>(p);
+      if (l1) contract_pipe<T, BN, 1, LA, LB, 0, false, G, X3><<<p.total_tiles, 256, 0, s>>>(p);
+      else contract_pipe<T, BN, 2, LA, LB, 0, false, G, X3><<<p.total_tiles, 256, 0, s>>>(p);
     }
     return true;
   }
