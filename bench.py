@@ -14,8 +14,9 @@ es.einconv, the halo + convolution the reference runs through F.conv2d;
 ``partition`` and ``roll`` are the reference's own local benchmarks of a family
 permute and of einroll (benchmarks/bench_local.py, "large" size).  ``copy`` and
 ``dma_calib`` calibrate the traffic counters; ``vendor_c1``, ``vendor_c2`` and
-``vendor_c4`` time torch's own GPU path (hipBLASLt) on configs 1, 2 and 4 as
-reference points.  ``all`` runs every workload but the calibrations and
+``vendor_c4`` time torch's own GPU path (hipBLASLt) on configs 1, 2 and 4, and
+``vendor_partition`` and ``vendor_roll`` torch's own device copy of the same bytes
+as ``partition`` and ``roll``, as reference points.  ``all`` runs every workload but the calibrations and
 reference points.
 
 Timing: W untimed warm-up steps, then K back-to-back steps between two device
@@ -372,6 +373,27 @@ def wl_vendor_c2(dev):
     return wl
 
 
+def _vendor_copy(wl, key, what):
+    """Reference point, not this library: torch's own device copy (``Tensor.clone`` of a
+    contiguous tensor, hipMemcpyAsync device to device) of the same bytes as ``wl``."""
+    wl.update(
+        key=key,
+        workload=f"reference: torch clone (hipMemcpyAsync device to device) of {what}'s input, the same bytes",
+        gpu_call=lambda es, xs: xs[0].clone(),
+        kernel_name="torch clone (hipMemcpyAsync)",
+        cpu_call=lambda xs: xs[0].clone(),
+    )
+    return wl
+
+
+def wl_vendor_roll(dev):
+    return _vendor_copy(wl_roll(dev), "vendor_roll", "roll")
+
+
+def wl_vendor_partition(dev):
+    return _vendor_copy(wl_partition(dev), "vendor_partition", "partition")
+
+
 WORKLOADS = {
     "c1": wl_c1,
     "c2": wl_c2,
@@ -388,6 +410,8 @@ WORKLOADS = {
     "vendor_c1": wl_vendor_c1,
     "vendor_c2": wl_vendor_c2,
     "vendor_c4": wl_vendor_c4,
+    "vendor_partition": wl_vendor_partition,
+    "vendor_roll": wl_vendor_roll,
 }
 
 
@@ -678,7 +702,7 @@ def main(argv=None):
     import torch_einshard as es
 
     dev = torch.device("cuda:0")
-    calibration = ("copy", "dma_calib", "vendor_c1", "vendor_c2", "vendor_c4")
+    calibration = ("copy", "dma_calib", "vendor_c1", "vendor_c2", "vendor_c4", "vendor_partition", "vendor_roll")
     keys = [k for k in sorted(WORKLOADS) if k not in calibration] if args.workload == "all" else [args.workload]
     for key in keys:
         line = bench_one(es, key, dev, args.steps, args.warmup, cpu=not args.no_cpu)
