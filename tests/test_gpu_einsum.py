@@ -233,15 +233,18 @@ def test_gemm_layouts(gpu, m, n, k, layout, dtype):
 
 @pytest.mark.parametrize("layout", ["nt", "nn", "tn", "tt"])
 @pytest.mark.parametrize("m, n, k", [(200, 136, 96), (64, 64, 32), (1024, 1024, 1024), (36, 1000, 4096)])
-def test_fp32_four_stage_kernel(gpu, m, n, k, layout):
-    # fp32 on 64 x 64 tiles: both operands copied by LDS-DMA in their own layout
-    # (K-contiguous or contiguous along M / N), four stages; ragged M and N edges
+def test_fp32_64x64_kernels(gpu, m, n, k, layout):
+    # fp32 on 64 x 64 tiles, both operands copied by LDS-DMA in their own layout
+    # (K-contiguous or contiguous along M / N); ragged M and N edges.  A K-contiguous x
+    # takes the four-wave pipelined kernel (w either way), an M-contiguous one the
+    # eight-wave kernel of six stages
     x = randn(m, k, seed=m + 5 * k)
     w = randn(n, k, seed=n + 7 * k)
     xd = x.to(gpu) if layout[0] == "n" else x.t().contiguous().to(gpu).t()
     wd = w.to(gpu) if layout[1] == "t" else w.t().contiguous().to(gpu).t()
     got = es.einshard("m k, n k -> m n", xd, wd)
-    assert _native.last_kernel() == "contract_f32_deep_64x64"
+    want_kernel = "contract_f32_pipe_64x64" if layout[0] == "n" else "contract_f32_deep_64x64"
+    assert _native.last_kernel() == want_kernel
     assert_rel(got, einshard_cpu("m k, n k -> m n", x, w), TOL[torch.float32])
 
 

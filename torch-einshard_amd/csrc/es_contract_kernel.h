@@ -2063,10 +2063,215 @@ __global__ __launch_bounds__(256 * KS, 1) void contract_f32_deep(const ContractA
   }
 }
 
+// ---- contract_f32_pipe: fp32 64 x 64 tiles on four waves, contract_pipe's schedule --
+// One 64 x 64 tile per work-group (C1: 256 tiles, one per CU), four waves of 32 x 32,
+// each 2 x 2 blocks of v_mfma_f32_16x16x4_f32: four accumulators, so consecutive MFMAs
+// never wait on each other's results.  A 32-deep K tile is two substeps of 16 k.  As in
+// contract_pipe, substep 0's MFMAs carry the fragment reads of substep 1; one barrier
+// (K tile kt+1 landed, every read of stage kt done); substep 1's MFMAs carry the copies
+// of K tile kt + NST into the stage just read and the fragment reads of K tile kt+1's
+// substep 0.  NST stages of 16 KB, filled by LDS-DMA in each operand's own layout:
+//   A (K-contiguous), and B when K-contiguous: 64 rows of 128 bytes, chunk c of row r
+//     at c ^ ((r / 2) % 8) (swz); a fragment (4 consecutive k of one row) is one
+//     16-byte read;
+//   B when N-contiguous: 32 k-rows of 64 floats, 16-byte chunk c of k-row r at
+//     c ^ (4 ((r / 4) % 4)); a fragment is 4 single-float reads, and the 4 k-rows a
+//     read touches (4 apart) put their 16 lanes on distinct banks.
+// Lane l of every fragment holds k = 16 ks + 4 (l / 16) + 0..3 for A and B alike, so
+// every product is formed once.  The MFMA's first operand is B's, so the accumulator
+// holds C^T: lane l ends with 4 consecutive n of one m, one 16-byte store.
+// With one wave per SIMD nothing hides a stall, hence the explicit interleave: the
+// simpler schedule (registers ring of loads, one write into LDS and one barrier per K
+// tile, then all of the tile's MFMAs) measured 30.5 us on C1 against 29.7 for
+// contract_f32_deep, 28.7 with its loads removed.
+// Bounded groups only (G sub-axes per group, ContractArgs::gdims) and at most two K
+// levels; the host guarantees whole 32-deep K tiles and (N-contiguous B) rows in
+// groups of 4.
+template <int LAYOUT, int SIDE, int G>
+struct F32PipeCopies {  // an 8 KB operand tile: two 1 KB copies per wave
+  static constexpr int NI = 2;
+  const float* src[NI];
+  int region0;
+  __device__ __forceinline__ void init(const ContractArgs& p, int wave, int lane, uint32_t row0, int64_t boff) {
+    region0 = wave * NI;
+    const GroupArgs& g = SIDE == 0 ? p.gm : p.gn;
+    const float* base = static_cast<const float*>(SIDE == 0 ? p.a : p.b);
+    const int64_t kstride = SIDE == 0 ? p.ka_inner : p.kb_inner;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int q = region0 + i;
+      if constexpr (LAYOUT == kKContig) {
+        // 8 rows of 128 bytes: lane l -> row 8 q + l / 8, stored chunk l % 8
+        const uint32_t lim = (SIDE == 0 ? p.M : p.N) - 1;
+        const int row = q * 8 + lane / kChunks;
+        uint32_t r = row0 + row;
+        r = r > lim ? lim : r;  // rows past the edge re-read the last row; never stored
+        src[i] = base + boff + group_offset_d<SIDE, G>(g, r) + swz(row, lane % kChunks) * 4;
+      } else {
+        // 4 k-rows of 256 bytes: lane l -> k-row 4 q + l / 16 at chunk position l % 16,
+        // which holds chunk (l % 16) ^ (4 (q % 4)) of the k-row
+        const uint32_t lim = (SIDE == 0 ? p.M : p.N) - 4;  // the last whole group of 4
+        const int krow = q * 4 + lane / 16;
+        const int chunk = (lane % 16) ^ (4 * (q & 3));
+        uint32_t r = row0 + 4 * chunk;
+        r = r > lim ? lim : r;
+        src[i] = base + boff + group_offset_d<SIDE, G>(g, r) + int64_t(krow) * kstride;
+      }
+    }
+  }
+  __device__ __forceinline__ void issue(int i, float* dst, int64_t koff) const {
+    copy_to_lds_v(src[i] + koff, lds_address(dst + (region0 + i) * 256));
+  }
+};
+
+// v_mfma_f32_16x16x4_f32 as inline assembly with the accumulator tied (see PipeMma)
+__device__ __forceinline__ void f32_mma(f32x4& acc, float n, float m) {
+  asm volatile("v_mfma_f32_16x16x4_f32 %0, %1, %2, %0" : "+a"(acc) : "v"(n), "v"(m));
+}
+__device__ __forceinline__ void f32_mma_first(f32x4& acc, float n, float m) {
+  asm volatile("v_mfma_f32_16x16x4_f32 %0, %1, %2, 0" : "=a"(acc) : "v"(n), "v"(m));
+}
+
+template <int LB, int L, int G, int NST = 3>
+__global__ __launch_bounds__(256, 1) void contract_f32_pipe(const ContractArgs p) {
+  static_assert(G > 0 && NST >= 3, "bounded groups; a stage being read, one landing, one in flight");
+  constexpr int TILE = 64 * 32, STAGE = 2 * TILE;  // floats: A's tile, then B's
+  constexpr int NCOPY = 4;                          // copies per wave per K tile
+  __shared__ __attribute__((aligned(1024))) float lds[NST * STAGE];
+  const int tid = threadIdx.x, lane = tid % 64;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int wm = wave / 2, wn = wave % 2;
+  uint32_t bidx, tm, tn;
+  tile_of(p, blockIdx.x, bidx, tm, tn);
+  const uint32_t m0 = tm * 64, n0 = tn * 64;
+  const int64_t boff_a = group_offset_d<0, G>(p.gb, bidx);
+  const int64_t boff_b = group_offset_d<1, G>(p.gb, bidx);
+  const int64_t boff_c = group_offset_d<2, G>(p.gb, bidx);
+  F32PipeCopies<kKContig, 0, G> ca;
+  F32PipeCopies<LB, 1, G> cb;
+  ca.init(p, wave, lane, m0, boff_a);
+  cb.init(p, wave, lane, n0, boff_b);
+  const uint32_t nk = p.K / 32;  // >= 1: an empty K takes the generic kernel
+  PipeWalk<L> w;  // the next K tile to copy (stays on the last one)
+  w.start(p);
+  auto copy = [&](int q, float* st) {
+    if (q < 2) ca.issue(q, st, w.oa);
+    else cb.issue(q - 2, st + TILE, w.ob);
+  };
+  const int g = lane / 16;
+  auto read_a = [&](const float* st, int i, int ks) -> f32x4 {
+    const int row = wm * 32 + 16 * i + lane % 16;
+    return *reinterpret_cast<const f32x4*>(st + row * 32 + swz(row, 4 * ks + g) * 4);
+  };
+  auto read_b = [&](const float* st, int j, int ks) -> f32x4 {
+    if constexpr (LB == kKContig) {
+      const int row = wn * 32 + 16 * j + lane % 16;
+      return *reinterpret_cast<const f32x4*>(st + TILE + row * 32 + swz(row, 4 * ks + g) * 4);
+    } else {
+      const int n = wn * 32 + 16 * j + lane % 16;
+      const float* b = st + TILE + (16 * ks + 4 * g) * 64 + ((n / 4) ^ (4 * g)) * 4 + n % 4;
+      return f32x4{b[0], b[64], b[128], b[192]};
+    }
+  };
+#pragma unroll
+  for (int t = 0; t < NST; ++t) {
+#pragma unroll
+    for (int q = 0; q < NCOPY; ++q) copy(q, lds + t * STAGE);
+    w.advance(nk);
+  }
+  f32x4 acc[2][2];  // first written by f32_mma_first
+  f32x4 af[2][2], bf[2][2];
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NST - 1) * NCOPY) : "memory");  // K tile 0 landed
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) af[0][i] = read_a(lds, i, 0);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) bf[0][j] = read_b(lds, j, 0);
+  // MFMA q of a substep: k-step s = q / 4, block (i, j) = ((q / 2) % 2, q % 2)
+  auto step = [&](uint32_t kt, auto first) {
+    float* cur = lds + (kt % NST) * STAGE;
+    const float* nxt = lds + ((kt + 1) % NST) * STAGE;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int s = q / 4, i = (q / 2) % 2, j = q % 2;
+      if (decltype(first)::value && s == 0) f32_mma_first(acc[i][j], bf[0][j][s], af[0][i][s]);
+      else f32_mma(acc[i][j], bf[0][j][s], af[0][i][s]);
+      if (q % 4 == 1) {  // substep 1's fragments: a0, a1, b0, b1
+        const int r = q / 4;
+        if (r < 2) af[1][r] = read_a(cur, r, 1);
+        else bf[1][r - 2] = read_b(cur, r - 2, 1);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NST - 2) * NCOPY) : "memory");  // K tile kt+1 landed
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int s = q / 4, i = (q / 2) % 2, j = q % 2;
+      f32_mma(acc[i][j], bf[1][j][s], af[1][i][s]);
+      if (q % 4 == 0) copy(q / 4, cur);  // K tile kt + NST into this stage
+      if (q % 4 == 2) {                   // K tile kt+1's substep 0 fragments
+        const int r = q / 4;
+        if (r < 2) af[0][r] = read_a(nxt, r, 0);
+        else bf[0][r - 2] = read_b(nxt, r - 2, 0);
+      }
+    }
+    w.advance(nk);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  step(0u, std::integral_constant<bool, true>{});
+  for (uint32_t kt = 1; kt < nk; ++kt) step(kt, std::integral_constant<bool, false>{});
+  pipe_drain(acc);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // lane: acc[i][j] = C[m = wm*32 + 16 i + lane%16][n = wn*32 + 16 j + 4 (lane/16) + 0..3]
+  float* C = static_cast<float*>(p.c);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t m = m0 + wm * 32 + 16 * i + lane % 16;
+    if (m >= p.M) continue;
+    const int64_t ro = boff_c + group_offset_d<2, G>(p.gm, m);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t n = n0 + wn * 32 + 16 * j + 4 * g;
+      if (n >= p.N) continue;
+      f32x4 v = acc[i][j];
+      if (p.bias != nullptr) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] += bias_at<float>(p, n + r);
+      }
+      if (p.vstore == 1) {  // n .. n + 3 contiguous and inside N (N's innermost extent % 4 == 0)
+        *reinterpret_cast<f32x4*>(C + ro + group_offset_d<2, G>(p.gn, n)) = v;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < p.N) C[ro + group_offset_d<2, G>(p.gn, n + r)] = v[r];
+      }
+    }
+  }
+}
+
+template <int LB, int L, int G>
+void launch_f32_pipe(const ContractArgs& p, hipStream_t s) {
+  contract_f32_pipe<LB, L, G><<<p.total_tiles, 256, 0, s>>>(p);
+}
+
 template <typename T>
 int launch_f32_deep(const ContractArgs& p, int la, int lb, hipStream_t s) {
   if constexpr (std::is_same_v<T, float>) {
     constexpr int KS = 2, NT = 256 * KS;
+    // contract_f32_pipe: A K-contiguous, bounded groups, at most two K levels
+    if (la == kKContig && (lb == kKContig || lb == kMNContig) && p.gdims > 0 && p.klevels <= 2) {
+      const bool l1 = p.klevels == 1, g1 = p.gdims == 1;
+      if (lb == kKContig) {
+        if (l1) g1 ? launch_f32_pipe<kKContig, 1, 1>(p, s) : launch_f32_pipe<kKContig, 1, 2>(p, s);
+        else g1 ? launch_f32_pipe<kKContig, 2, 1>(p, s) : launch_f32_pipe<kKContig, 2, 2>(p, s);
+      } else {
+        if (l1) g1 ? launch_f32_pipe<kMNContig, 1, 1>(p, s) : launch_f32_pipe<kMNContig, 1, 2>(p, s);
+        else g1 ? launch_f32_pipe<kMNContig, 2, 1>(p, s) : launch_f32_pipe<kMNContig, 2, 2>(p, s);
+      }
+      set_kernel("contract_f32_pipe_64x64");
+      return check_launch("es_contract");
+    }
     if (la == kKContig && lb == kKContig) contract_f32_deep<kKContig, kKContig, KS><<<p.total_tiles, NT, 0, s>>>(p);
     else if (la == kKContig) contract_f32_deep<kKContig, kMNContig, KS><<<p.total_tiles, NT, 0, s>>>(p);
     else if (lb == kKContig) contract_f32_deep<kMNContig, kKContig, KS><<<p.total_tiles, NT, 0, s>>>(p);
