@@ -68,8 +68,9 @@ struct ContractArgs {
   FastDiv tdiv_batch;    // divides by the tiles of one batch entry (tiles_m * tiles_n)
   FastDiv tdiv_group;    // ... of one tile group (tiles_m * group_n)
   FastDiv tdiv_gn;       // ... by group_n
-  // the largest sub-axis count of gb, gm and gn when it is at most 2 (at least 1), else 0:
-  // contract_pipe's bounded-group instantiations unroll the offset walks to that many
+  // the largest sub-axis count of gb, gm and gn when it is at most 3 (at least 1), else 0:
+  // the bounded-group instantiations unroll the offset walks to that many (1 or 2; the
+  // halo kernel 3)
   int32_t gdims;
   uint32_t pipe_bn;      // 224: contract_pipe's 256 x 224 tiles; 0: 256 x 256
   int32_t vstore;        // 16-byte vector stores: 1 along n; 2 along m (contract_pipe only)

@@ -330,7 +330,7 @@ int contract(const es_contract_desc* d, const void* a, const void* b, const void
   p.tdiv_gn.init(p.group_n);
   {
     const int most = std::max(d->n_batch, std::max(d->n_m, d->n_n));
-    p.gdims = most <= 2 ? std::max(most, 1) : 0;
+    p.gdims = most <= 3 ? std::max(most, 1) : 0;
   }
   p.halo_n = 0;
   if (halo != nullptr && (st = halo_args(d, halo, esz, la, lb, config, bk, p)) != ES_OK) return st;

@@ -941,7 +941,8 @@ __device__ __forceinline__ void buffer_copy_to_lds(const u32x4& srd, uint32_t vo
 // dim; each lane keeps, for each of its rows, a mask with bit k set when that position
 // falls outside [0, extent_s) along some dim.  Such a copy's offset gets bit 31, past
 // the buffer's range, and loads zeros.  The K tile's offset rides in the scalar offset.
-template <typename S, int ROWS, int NW>
+// G > 0: M has at most G sub-axes (ContractArgs::gdims), walked by G - 1 divisions.
+template <typename S, int ROWS, int NW, int G = 0>
 struct PipeCopiesHalo {
   static constexpr int RPI = 64 / kChunks;  // rows per copy instruction
   static constexpr int NI = ROWS / RPI / NW;
@@ -963,14 +964,26 @@ struct PipeCopiesHalo {
       // one pass over M's sub-axes: the row's offset and its positions along the halo dims
       int64_t goff = boff;
       outer[i] = inner[i] = 0;
+      if constexpr (G > 0) {
+        // sub-axes G - 1 .. 1 by division (those past gm.n divide by 1), 0 the quotient left
 #pragma unroll
-      for (int d = ES_MAX_AXES - 1; d >= 0; --d) {
-        if (d < p.gm.n) {
-          uint32_t rem;
-          r = p.gm.div[d].divmod(r, rem);
+        for (int d = G - 1; d >= 0; --d) {
+          uint32_t rem = r;
+          if (d > 0) r = p.gm.div[d].divmod(r, rem);
           goff += int64_t(rem) * p.gm.sa[d];
           outer[i] = d == p.halo_mlev[0] ? rem : outer[i];
           inner[i] = d == p.halo_mlev[1] ? rem : inner[i];
+        }
+      } else {
+#pragma unroll
+        for (int d = ES_MAX_AXES - 1; d >= 0; --d) {
+          if (d < p.gm.n) {
+            uint32_t rem;
+            r = p.gm.div[d].divmod(r, rem);
+            goff += int64_t(rem) * p.gm.sa[d];
+            outer[i] = d == p.halo_mlev[0] ? rem : outer[i];
+            inner[i] = d == p.halo_mlev[1] ? rem : inner[i];
+          }
         }
       }
       off[i] = uint32_t(goff * int64_t(sizeof(S))) + uint32_t(chunk * 16);
@@ -1470,10 +1483,12 @@ __device__ __forceinline__ void store_pipe_f32(const ContractArgs& p, typename T
 // 1 and 2 is an instantiation of its own: with every epilogue in one function the
 // 256-wide kernel spilled accumulators to scratch.
 // HALO: A is read by PipeCopiesHalo (es_contract_halo), both operands K-contiguous.
-// G > 0: the batch, M and N groups have at most G sub-axes each (ContractArgs::gdims, no
-// halo): every row, column and batch offset is an unrolled walk of G - 1 divisions, so the
-// set-up in front of the first copies is a few hundred instructions instead of a walk over
-// ES_MAX_AXES sub-axes per row with a scalar load per step.
+// G > 0: the batch, M and N groups have at most G sub-axes each (ContractArgs::gdims; 1
+// or 2, or with a halo 3, for the batch, height and width of a 2-D convolution): every
+// row, column and batch offset is an unrolled walk of G - 1 divisions, so the set-up in
+// front of the first copies is a few hundred instructions instead of a walk over
+// ES_MAX_AXES sub-axes per row with a scalar load per step (the halo kernel of einconv's
+// benchmark: 2,605 instructions, 87 waits for scalar loads, 7-10 us per work-group).
 // X3 (no halo): one operand, the deep one (1: A, 2: B), gets three LDS stages and the
 // other two, so the deep operand's copies run two K tiles ahead (the other's one): in
 // step kt the copies of the other's tile kt+2 and the deep operand's tile kt+3 go into
@@ -1496,10 +1511,9 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   constexpr int STAGE = (BM + BN) * BK;
   constexpr int MMAS = FM * FN;  // per substep
   using CopyA = std::conditional_t<
-      HALO, PipeCopiesHalo<S, BM, WM * WN>,
+      HALO, PipeCopiesHalo<S, BM, WM * WN, G>,
       std::conditional_t<LA == kMNContig, PipeCopiesMN<S, BM, WM * WN, 0, G>, PipeCopies<S, BM, WM * WN, 0, G>>>;
   static_assert(!HALO || (LA == kKContig && LB == kKContig), "the halo reads K-contiguous operands");
-  static_assert(G == 0 || !HALO, "the halo copies walk the M group themselves");
   static_assert(X3 == 0 || (!HALO && (BN == 224 ? X3 == 1 && LA == kKContig && LB == kKContig : EPI == 1 && G > 0)),
                 "three stages: A of 224-wide K-contiguous tiles, or either of 256-wide tiles with EPI 1 and bounded groups");
   using CopyB =
@@ -2260,7 +2274,7 @@ int launch_f32_deep(const ContractArgs& p, int la, int lb, hipStream_t s) {
   if constexpr (std::is_same_v<T, float>) {
     constexpr int KS = 2, NT = 256 * KS;
     // contract_f32_pipe: A K-contiguous, bounded groups, at most two K levels
-    if (la == kKContig && (lb == kKContig || lb == kMNContig) && p.gdims > 0 && p.klevels <= 2) {
+    if (la == kKContig && (lb == kKContig || lb == kMNContig) && p.gdims > 0 && p.gdims <= 2 && p.klevels <= 2) {
       const bool l1 = p.klevels == 1, g1 = p.gdims == 1;
       if (lb == kKContig) {
         if (l1) g1 ? launch_f32_pipe<kKContig, 1, 1>(p, s) : launch_f32_pipe<kKContig, 1, 2>(p, s);
@@ -2288,6 +2302,12 @@ int launch_f32_deep(const ContractArgs& p, int la, int lb, hipStream_t s) {
 // tile with vector stores and a 16-bit output takes the one-pass epilogue
 template <typename T, int BN, int EPI>
 void launch_pipe_halo(const ContractArgs& p, hipStream_t s) {
+  // bounded groups: up to three M sub-axes (batch, height, width)
+  if (p.gdims > 0) {
+    if (p.klevels <= 2) contract_pipe<T, BN, 2, kKContig, kKContig, EPI, true, 3><<<p.total_tiles, 256, 0, s>>>(p);
+    else contract_pipe<T, BN, kKLevels, kKContig, kKContig, EPI, true, 3><<<p.total_tiles, 256, 0, s>>>(p);
+    return;
+  }
   if (p.klevels <= 2) contract_pipe<T, BN, 2, kKContig, kKContig, EPI, true><<<p.total_tiles, 256, 0, s>>>(p);
   else contract_pipe<T, BN, kKLevels, kKContig, kKContig, EPI, true><<<p.total_tiles, 256, 0, s>>>(p);
 }
@@ -2335,7 +2355,7 @@ bool launch_pipe_g(const ContractArgs& p, hipStream_t s) {
 // takes G = 1, where a row's offset is one multiply; up to two take G = 2
 template <typename T, int BN, int LA, int LB>
 bool launch_pipe_bounded(const ContractArgs& p, hipStream_t s) {
-  if (p.gdims == 0 || p.klevels > 2) return false;
+  if (p.gdims == 0 || p.gdims > 2 || p.klevels > 2) return false;
   if constexpr (LA == kKContig && LB == kKContig) {
     if (p.gdims == 1) return launch_pipe_g<T, BN, LA, LB, 1>(p, s);
   }
