@@ -248,6 +248,30 @@ def test_fp32_64x64_kernels(gpu, m, n, k, layout):
     assert_rel(got, einshard_cpu("m k, n k -> m n", x, w), TOL[torch.float32])
 
 
+@pytest.mark.parametrize("w_layout", ["k", "n"])
+@pytest.mark.parametrize("case", ["two K levels", "two M sub-axes", "both"])
+def test_fp32_pipelined_kernel_walks(gpu, case, w_layout):
+    # contract_f32_pipe's bounded walks: K in two sub-axes that do not merge (x stores b
+    # outside m: K levels (b, c)), M in two (x's a and e swapped in memory), ragged edges;
+    # w K-contiguous ([n, b, c]) or N-contiguous ([b, c, n])
+    m_axes = "a e" if case != "two K levels" else "m"
+    k_axes = "b c" if case != "two M sub-axes" else "c"
+    sizes = {"m": 200, "a": 10, "e": 20, "b": 3, "c": 64, "n": 136}
+    x_order = {"two K levels": "b m c", "two M sub-axes": "e a c", "both": "b e a c"}[case]
+    x_base = randn(*[sizes[v] for v in x_order.split()], seed=91)
+    x_logical = f"{m_axes} {k_axes}"
+    xd = x_base.to(gpu).permute(*[x_order.split().index(v) for v in x_logical.split()])
+    w_order = f"n {k_axes}" if w_layout == "k" else f"{k_axes} n"
+    w_base = randn(*[sizes[v] for v in w_order.split()], seed=92)
+    w_logical = f"n {k_axes}"
+    wd = w_base.to(gpu).permute(*[w_order.split().index(v) for v in w_logical.split()])
+    expr = f"{x_logical}, {w_logical} -> {m_axes} n"
+    got = es.einshard(expr, xd, wd)
+    assert _native.last_kernel() == "contract_f32_pipe_64x64", _native.last_kernel()
+    want = einshard_cpu(expr, xd.cpu().contiguous(), wd.cpu().contiguous())
+    assert_rel(got, want, TOL[torch.float32])
+
+
 def test_gemm_uses_fast_layouts(gpu):
     x = randn(512, 256, dtype=torch.bfloat16).to(gpu)
     w = randn(384, 256, dtype=torch.bfloat16).to(gpu)
