@@ -1490,12 +1490,14 @@ __device__ __forceinline__ void store_pipe_f32(const ContractArgs& p, typename T
 // ES_MAX_AXES sub-axes per row with a scalar load per step (the halo kernel of einconv's
 // benchmark: 2,605 instructions, 87 waits for scalar loads, 7-10 us per work-group).
 // X3 (no halo): one operand, the deep one (1: A, 2: B), gets three LDS stages and the
-// other two, so the deep operand's copies run two K tiles ahead (the other's one): in
-// step kt the copies of the other's tile kt+2 and the deep operand's tile kt+3 go into
-// the stages that step kt's first substep finished reading, the other's first, and the
-// barrier waits for all but the deep operand's last batch (loads complete in order).  On
-// a cold cache a copy from HBM takes longer than one K step; with one tile of lead the
-// loop waited for it.  The deep operand is the one with more rows of its own to stream
+// other two, so the deep operand's copies start a substep earlier: in step kt its tile
+// kt+2 goes, during the first substep, into the stage step kt-1 finished reading, and the
+// other operand's tile kt+2 goes, during the second, into the stage the first substep
+// finished reading.  The barrier waits for all but the deep operand's last batch (loads
+// complete in order).  On a cold cache a copy from HBM takes longer than one K step;
+// with one tile of lead the loop waited for it.  Splitting the copies over both
+// substeps also keeps the second substep from running long: with all of them in it
+// (the deep tile then kt+3), C4 took 193.0 us flushed against 189.9.  The deep operand is the one with more rows of its own to stream
 // (A for 16384 x 1792, B for 2048 x 8192).  224-wide tiles: A, with both operands
 // K-contiguous.  256-wide tiles (EPI 1): the ring takes all 160 KB of LDS, so the
 // epilogue's offset tables wait in registers through the K loop and go to LDS after it.
@@ -1652,10 +1654,9 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
     auto b_stage = [&](uint32_t j) { return lds0 + NA * A_TILE + j * B_TILE; };
     PipeWalk<L> wd;  // the deep operand's next K tile to copy
     wd.start(p);
-    // the other operand's next K tile (from step 0 on) is the one before the deep
-    // operand's: its offset is the walk's, kept from before the walk's last advance
+    // both operands copy the same K tile in a step (the deep one in substep 0, the other
+    // in substep 1): the other operand's offset is the walk's
     auto other_off = [&]() { return X3 == 1 ? wd.ob : wd.oa; };
-    int64_t o_off = 0;
     constexpr int NI_D = X3 == 1 ? CopyA::NI : CopyB::NI;  // copies per K tile: deep operand
     constexpr int NI_O = NCOPY - NI_D;                      // ... and the other
     // copy q of the deep (other) operand's next K tile into its stage `st`
@@ -1672,8 +1673,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
       else
         ca.issue_one(q, static_cast<const S*>(p.a) + off, ring_addr + st * uint32_t(A_TILE * sizeof(S)));
     };
-    // K tiles 0 and 1 of both operands and the deep operand's tile 2, in the order the
-    // barriers count them: D0 O0 | O1 D1 | D2
+    // K tiles 0 and 1 of both operands, in the order the barriers count them: D0 O0 | O1 D1
 #pragma unroll
     for (int q = 0; q < NI_D; ++q) copy_d(q, 0);
 #pragma unroll
@@ -1684,12 +1684,8 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
 #pragma unroll
     for (int q = 0; q < NI_D; ++q) copy_d(q, 1);
     wd.advance(nk);
-#pragma unroll
-    for (int q = 0; q < NI_D; ++q) copy_d(q, 2);
-    o_off = other_off();
-    wd.advance(nk);
     pre_tables();
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY + NI_D) : "memory");  // K tile 0 landed
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY) : "memory");  // K tile 0 landed
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < FM; ++i) af[0][i] = fa.read(a_stage(0), i, 0);
@@ -1699,10 +1695,15 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
     auto step3 = [&](uint32_t d_cur, uint32_t d_nxt, uint32_t o_cur, uint32_t o_nxt, auto first) {
       const S* as = a_stage(X3 == 1 ? d_cur : o_cur);
       const S* bs = b_stage(X3 == 1 ? o_cur : d_cur);
+      const uint32_t d_far = 3u - d_cur - d_nxt;  // the deep stage step kt - 1 finished with
 #pragma unroll
       for (int q = 0; q < MMAS; ++q) {
         if constexpr (decltype(first)::value) PipeMma<T>::mma_first(acc[q / FN][q % FN], bf[0][q % FN], af[0][q / FN]);
         else PipeMma<T>::mma(acc[q / FN][q % FN], bf[0][q % FN], af[0][q / FN]);
+        {  // the deep operand's tile kt + 2 into it
+          const int c0 = (q * NI_D) / MMAS, c1 = ((q + 1) * NI_D) / MMAS;
+          if (c0 != c1) copy_d(c0, d_far);
+        }
         const int r0 = (q * (FM + FN)) / MMAS, r1 = ((q + 1) * (FM + FN)) / MMAS;
         if (r0 != r1) {
           if (r0 < FM) af[1][r0] = fa.read(as, r0, 1);
@@ -1719,19 +1720,15 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
 #pragma unroll
       for (int q = 0; q < MMAS; ++q) {
         PipeMma<T>::mma(acc[q / FN][q % FN], bf[1][q % FN], af[1][q / FN]);
-        // the other operand's tile kt+2 into o_cur, then the deep operand's kt+3 into d_cur
-        const int c0 = (q * NCOPY) / MMAS, c1 = ((q + 1) * NCOPY) / MMAS;
-        if (c0 != c1) {
-          if (c0 < NI_O) copy_o(c0, o_cur, o_off);
-          else copy_d(c0 - NI_O, d_cur);
-        }
+        // the other operand's tile kt + 2 into o_cur
+        const int c0 = (q * NI_O) / MMAS, c1 = ((q + 1) * NI_O) / MMAS;
+        if (c0 != c1) copy_o(c0, o_cur, other_off());
         const int r0 = (q * (FM + FN)) / MMAS, r1 = ((q + 1) * (FM + FN)) / MMAS;
         if (r0 != r1) {
           if (r0 < FM) af[0][r0] = fa.read(an, r0, 0);
           else bf[0][r0 - FM] = fb.read(bn, r0 - FM, 0);
         }
       }
-      o_off = other_off();
       wd.advance(nk);
       __builtin_amdgcn_sched_barrier(0);
     };
