@@ -1285,8 +1285,10 @@ __device__ __forceinline__ void store_pipe(const ContractArgs& p, typename Trait
 // with 16-byte streaming stores.  The offset tables (`tables`, BM + 256 entries) have
 // 4 KB of LDS of their own; PRE: the caller formed them before its K loop (as here), so
 // the epilogue reads no kernel argument (after 100 us of K loop such a scalar load misses
-// every cache, and a few of them in a row measured 1-2 us per tile).  C is the output.
-template <typename T, int BN, int FM, int FN, bool BIAS, int G = 0, bool PRE = false>
+// every cache, and a few of them in a row measured 1-2 us per tile).  BIAS_LDS: the
+// bias, as floats, sits in LDS after the tables (contract_pipe's kBiasLds).  C is the
+// output.
+template <typename T, int BN, int FM, int FN, bool BIAS, int G = 0, bool PRE = false, bool BIAS_LDS = false>
 __device__ __forceinline__ void store_pipe_wide(const ContractArgs& p, typename Traits<T>::S* lds0,
                                                 typename Traits<T>::S* lds1, const f32x4 (&acc)[FM][FN],
                                                 uint32_t m0, uint32_t n0, int64_t boff_c, int64_t* tables,
@@ -1304,11 +1306,16 @@ __device__ __forceinline__ void store_pipe_wide(const ContractArgs& p, typename 
   const int wm = wave / 2;
   const int wn = wave % 2;
   // the bias loads go first, so their latency passes while the offset tables are formed
+  // (BIAS_LDS: the caller put the tile's bias, as floats, in LDS after the tables)
+  const float* bias_lds = reinterpret_cast<const float*>(tables + BM + 256);
   f32x4 bv[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) bv[j][r] = BIAS ? bias_at<T>(p, n0 + wn * WTN + j * 16 + 4 * (lane / 16) + r) : 0.f;
+    for (int r = 0; r < 4; ++r) {
+      const int c = wn * WTN + j * 16 + 4 * (lane / 16) + r;
+      bv[j][r] = !BIAS ? 0.f : (BIAS_LDS ? bias_lds[c] : bias_at<T>(p, n0 + c));
+    }
   if constexpr (!PRE) {
     const KArgs kp = kernel_args();
     const uint32_t m = m0 + tid, n = n0 + tid;
@@ -1540,7 +1547,8 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   constexpr int STAGES_BYTES = (X3 ? RING : 2 * STAGE_ALLOC) * int(sizeof(S));
   // the one-pass epilogue's row and column offset tables: LDS of their own when that fits
   // beside the stages, else (a 256-wide ring) the ring's bytes past the staged halves
-  constexpr int TABLE_BYTES = (BM + 256) * int(sizeof(int64_t));
+  // ... and, EPI 1, the tile's bias as floats after them
+  constexpr int TABLE_BYTES = (BM + 256) * int(sizeof(int64_t)) + (EPI == 1 ? 256 * int(sizeof(float)) : 0);
   constexpr bool kOwnTables = EPI == 1 && STAGES_BYTES + TABLE_BYTES <= kLdsBytes;
   static_assert(EPI != 1 || kOwnTables || 2 * 128 * 256 * int(sizeof(S)) + TABLE_BYTES <= STAGES_BYTES, "tables fit");
   __shared__ __attribute__((aligned(1024))) char lds_raw[STAGES_BYTES + (kOwnTables ? TABLE_BYTES : 0)];
@@ -1554,6 +1562,11 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   // the bias test in scalar registers through the K loop: the epilogue then reads no
   // kernel argument
   constexpr bool kPreTables = EPI == 1 && G > 0;
+  // the bias of the tile's columns, loaded ahead of the first copies (so the prologue's
+  // wait covers it) and put in LDS beside the tables: the epilogue then reads it from LDS
+  // instead of from memory after the K loop (the tables' own LDS only)
+  constexpr bool kBiasLds = kPreTables && kOwnTables;
+  float* const ep_bias = reinterpret_cast<float*>(ep_tables + BM + 256);
   int64_t reg_row = -1, reg_col = -1;
 
   const int tid = threadIdx.x;
@@ -1625,6 +1638,20 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
       cb.issue_one(q - CopyA::NI, static_cast<const S*>(p.b) + w.ob, stage + uint32_t(BM * BK * sizeof(S)));
     }
   };
+  // kBiasLds: the bias loads go out ahead of the first copies; their values reach LDS
+  // right after the wait for K tile 0 (the compiler's own wait for them then also covers
+  // K tile 1's copies, which were issued right after tile 0's)
+  float reg_bias = 0.f;
+  auto bias_load = [&]() {
+    if constexpr (kBiasLds) {
+      if (p.bias != nullptr && tid < BN) reg_bias = bias_at<T>(p, n0 + tid);
+    }
+  };
+  auto bias_store = [&]() {
+    if constexpr (kBiasLds) {
+      if (tid < BN) ep_bias[tid] = reg_bias;
+    }
+  };
   // the epilogue's output pointer and bias test (see kPreTables)
   S* out_c;
   uint32_t has_bias;
@@ -1674,6 +1701,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
         ca.issue_one(q, static_cast<const S*>(p.a) + off, ring_addr + st * uint32_t(A_TILE * sizeof(S)));
     };
     // K tiles 0 and 1 of both operands, in the order the barriers count them: D0 O0 | O1 D1
+    bias_load();
 #pragma unroll
     for (int q = 0; q < NI_D; ++q) copy_d(q, 0);
 #pragma unroll
@@ -1686,6 +1714,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
     wd.advance(nk);
     pre_tables();
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY) : "memory");  // K tile 0 landed
+    bias_store();
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < FM; ++i) af[0][i] = fa.read(a_stage(0), i, 0);
@@ -1747,6 +1776,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
     }
     for (; kt < nk; ++kt) step3(kt % 3, (kt + 1) % 3, kt % 2, (kt + 1) % 2, Next{});
   } else {
+  bias_load();
   halo_voffs();
 #pragma unroll
   for (int q = 0; q < NCOPY; ++q) copy(q, lds0_addr);
@@ -1757,6 +1787,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   w.advance(nk);
   pre_tables();
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCOPY) : "memory");  // K tile 0 of this wave landed
+  bias_store();
   __syncthreads();
   frags(lds0, 0, 0);
 
@@ -1818,7 +1849,8 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
       if (tid < BN) ep_tables[BM + tid] = reg_col;
     }
     if (has_bias)
-      store_pipe_wide<T, BN, FM, FN, true, G, kPreTables>(p, lds0, lds1, acc, m0, n0, boff_c, ep_tables, out_c);
+      store_pipe_wide<T, BN, FM, FN, true, G, kPreTables, kBiasLds>(p, lds0, lds1, acc, m0, n0, boff_c, ep_tables,
+                                                                    out_c);
     else
       store_pipe_wide<T, BN, FM, FN, false, G, kPreTables>(p, lds0, lds1, acc, m0, n0, boff_c, ep_tables, out_c);
     return;
