@@ -365,6 +365,10 @@ def test_repeated_calls_replay_with_fresh_data_and_geometry(gpu):
         ("m k, k n -> m n", [(4096, 128), (128, 4096)], "contract_pipe_256x256_mn_b"),
         ("k m, k n -> m n", [(192, 4096), (192, 4136)], "contract_pipe_256x256_mn_ab"),
         ("k m, n k -> m n", [(128, 4136), (4000, 128)], "contract_pipe_256x256_mn_a"),
+        # more N rows than M rows: B takes the third LDS stage (K-contiguous operands, and
+        # an N-contiguous B with a ragged N edge)
+        ("m k, n k -> m n", [(2048, 192), (8192, 192)], "contract_pipe_256x256"),
+        ("m k, k n -> m n", [(2048, 128), (128, 8104)], "contract_pipe_256x256_mn_b"),
     ],
 )
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
