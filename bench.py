@@ -17,7 +17,11 @@ permute and of einroll (benchmarks/bench_local.py, "large" size).  ``copy`` and
 ``vendor_c4`` time torch's own GPU path (hipBLASLt) on configs 1, 2 and 4, and
 ``vendor_partition`` and ``vendor_roll`` torch's own device copy of the same bytes
 as ``partition`` and ``roll``, as reference points.  ``all`` runs every workload but the calibrations and
-reference points.
+reference points.  ``--vs-vendor`` (with c1, c2 or c4) times this library's launch and
+the workload's reference point alternately on the same inputs, warm and flushed, the
+order swapped every round, so both see the same clock and power state of the board
+(dispatch times of either climb by up to 40 % and fall back over a run as the board
+limits its power); it prints one line with both.
 
 Timing: W untimed warm-up steps, then K back-to-back steps between two device
 synchronisations (wall clock -> ms_per_step, value: host work included).  The
@@ -470,8 +474,6 @@ def _measure_gpu(es, wl, dev, steps, warmup):
     run = _runner(es, wl)
     for _ in range(warmup):
         run(xs)
-    stream = torch.cuda.current_stream(dev)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -479,11 +481,23 @@ def _measure_gpu(es, wl, dev, steps, warmup):
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - t0
     del out
-    # kernel time: the same K launches behind a bounded spin kernel, so that the
-    # host has enqueued all of them before the first starts and the two events
-    # bracket back-to-back kernels only (no host gaps)
     run, xs = _kernel_runner(es, wl, xs)
-    out = run(xs)
+    run(xs)
+    kernel_ms = _time_warm(run, xs, dev, steps)
+    flush = _flush_buffer(dev)
+    cold_ms = _time_flushed(run, xs, dev, steps, flush)
+    del flush
+    from torch_einshard import _native
+
+    return dict(wall_s=wall, kernel_ms=kernel_ms, cold_ms=cold_ms, kernel=wl.get("kernel_name") or _native.last_kernel())
+
+
+def _time_warm(run, xs, dev, steps):
+    """ms per launch of K launches queued behind a bounded spin kernel, so that the host
+    has enqueued all of them before the first starts and the two events bracket
+    back-to-back kernels only (no host gaps)."""
+    stream = torch.cuda.current_stream(dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize(dev)
     torch.cuda._sleep(PRIME_CYCLES)
     start.record(stream)
@@ -491,17 +505,26 @@ def _measure_gpu(es, wl, dev, steps, warmup):
         out = run(xs)
     end.record(stream)
     torch.cuda.synchronize(dev)
-    kernel_ms = start.elapsed_time(end) / steps
     del out
-    # the same launches, each after the 256 MB Infinity Cache and the L2s are
-    # flushed by a 512 MiB read (a read leaves no dirty lines behind to be written
-    # back during the launch; float32, since a sum of int32 would first convert to
-    # int64, writing 1 GiB).  The launch's cost is the difference of two batches
-    # timed the same way: K x (flush, launch) and K x flush, each queued behind the
-    # spin kernel.  An event pair around every single launch would add ~5-8 us of
-    # event overhead per launch (checked against rocprofv3 kernel durations).
+    return start.elapsed_time(end) / steps
+
+
+def _flush_buffer(dev):
+    """512 MiB read by every flush: it evicts the 256 MB Infinity Cache and the L2s and
+    leaves no dirty lines behind to be written back during the next launch (float32,
+    since a sum of int32 would first convert to int64, writing 1 GiB)."""
     flush = torch.ones(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
     flush.sum()
+    return flush
+
+
+def _time_flushed(run, xs, dev, steps, flush):
+    """ms per launch, each launch right after a flush: the difference of two batches timed
+    the same way, K x (flush, launch) and K x flush, each queued behind the spin kernel.
+    An event pair around every single launch would add ~5-8 us of event overhead per
+    launch (checked against rocprofv3 kernel durations)."""
+    stream = torch.cuda.current_stream(dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
     def batch(with_kernel):
         torch.cuda.synchronize(dev)
@@ -516,11 +539,51 @@ def _measure_gpu(es, wl, dev, steps, warmup):
         return start.elapsed_time(end)
 
     both, alone = batch(True), batch(False)
-    cold_ms = (both - alone) / steps
-    del flush
-    from torch_einshard import _native
+    return (both - alone) / steps
 
-    return dict(wall_s=wall, kernel_ms=kernel_ms, cold_ms=cold_ms, kernel=wl.get("kernel_name") or _native.last_kernel())
+
+def measure_vs_vendor(es, key, dev, steps, warmup, rounds):
+    """This library's launch and torch's own GPU path for the same workload (``vendor_<key>``:
+    hipBLASLt), timed alternately on the same inputs: each round times both, warm and
+    flushed, the order swapped every round, so that both see the same clock and power
+    state of the board.  Returns one JSON-ready dict with every round's figures."""
+    wl, vendor = WORKLOADS[key](dev), WORKLOADS[f"vendor_{key}"](dev)
+    xs = [t.to(dev) for t in wl["host"]]
+    legs = {"einshard": _runner(es, wl), "vendor": _runner(es, vendor)}
+    gc.collect()
+    gc.disable()
+    try:
+        for _ in range(warmup):
+            for run in legs.values():
+                run(xs)
+        from torch_einshard import _native
+
+        legs["einshard"](xs)
+        kernel = _native.last_kernel()
+        flush = _flush_buffer(dev)
+        times = {name: {"warm_ms": [], "flushed_ms": []} for name in legs}
+        for r in range(rounds):
+            order = list(legs) if r % 2 == 0 else list(legs)[::-1]
+            for name in order:
+                times[name]["warm_ms"].append(round(_time_warm(legs[name], xs, dev, steps), 5))
+                times[name]["flushed_ms"].append(round(_time_flushed(legs[name], xs, dev, steps, flush), 5))
+        del flush
+    finally:
+        gc.enable()
+    med = lambda v: sorted(v)[len(v) // 2]
+    out = {
+        "metric": "kernel ms per launch, this library against torch's GPU path, timed alternately",
+        "workload": wl["workload"],
+        "reference": vendor["workload"],
+        "steps": steps,
+        "rounds": rounds,
+        "kernel": kernel,
+    }
+    for name, t in times.items():
+        out[name] = dict(t, warm_ms_median=med(t["warm_ms"]), flushed_ms_median=med(t["flushed_ms"]))
+    for mode in ("warm", "flushed"):
+        out[f"ratio_{mode}"] = round(out["einshard"][f"{mode}_ms_median"] / out["vendor"][f"{mode}_ms_median"], 4)
+    return out
 
 
 def measure_cpu(wl, budget_s=12.0):
@@ -688,6 +751,12 @@ def main(argv=None):
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default="c4", choices=sorted(WORKLOADS) + ["all"])
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    parser.add_argument(
+        "--vs-vendor",
+        action="store_true",
+        help="time the workload (c1, c2 or c4) and torch's GPU path on it alternately; one JSON line",
+    )
+    parser.add_argument("--rounds", type=int, default=6, help="alternations of --vs-vendor")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(
@@ -702,6 +771,14 @@ def main(argv=None):
     import torch_einshard as es
 
     dev = torch.device("cuda:0")
+    if args.vs_vendor:
+        if f"vendor_{args.workload}" not in WORKLOADS:
+            print(f"bench.py: --vs-vendor needs a workload with a vendor_ reference point, not {args.workload}",
+                  file=sys.stderr)
+            return 2
+        line = measure_vs_vendor(es, args.workload, dev, args.steps, args.warmup, args.rounds)
+        print(json.dumps(line), flush=True)
+        return 0
     calibration = ("copy", "dma_calib", "vendor_c1", "vendor_c2", "vendor_c4", "vendor_partition", "vendor_roll")
     keys = [k for k in sorted(WORKLOADS) if k not in calibration] if args.workload == "all" else [args.workload]
     for key in keys:
