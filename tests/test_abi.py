@@ -53,8 +53,9 @@ def test_library_loads_and_reports_version():
 
 
 def _integration_stub_classes():
-    """The ctypes classes of INTEGRATION.md's binding example, executed without the
-    library (the CDLL line and everything after the classes are left out)."""
+    """The ctypes classes of the binding example in the repository's integration guide
+    (the file read below), executed without the library (the CDLL line and everything
+    after the classes are left out)."""
     doc = os.path.join(os.path.dirname(HEADER), os.pardir, "INTEGRATION.md")
     text = open(doc).read()
     block = next(b for b in re.findall(r"```python\n(.*?)```", text, flags=re.S) if "class es_axis" in b)
