@@ -14,10 +14,11 @@ es.einconv, the halo + convolution the reference runs through F.conv2d;
 ``partition`` and ``roll`` are the reference's own local benchmarks of a family
 permute and of einroll (benchmarks/bench_local.py, "large" size).  ``copy`` and
 ``dma_calib`` calibrate the traffic counters; ``vendor_c1``, ``vendor_c2`` and
-``vendor_c4`` time torch's own GPU path (hipBLASLt) on configs 1, 2 and 4, and
+``vendor_c4`` time torch's own GPU path (hipBLASLt) on configs 1, 2 and 4,
+``vendor_conv`` the reference's GPU path of einconv (F.pad, F.conv2d on MIOpen), and
 ``vendor_partition`` and ``vendor_roll`` torch's own device copy of the same bytes
 as ``partition`` and ``roll``, as reference points.  ``all`` runs every workload but the calibrations and
-reference points.  ``--vs-vendor`` (with c1, c2 or c4) times this library's launch and
+reference points.  ``--vs-vendor`` (with c1, c2, c4 or conv) times this library's launch and
 the workload's reference point alternately on the same inputs, warm and flushed, the
 order swapped every round, so both see the same clock and power state of the board
 (dispatch times of either climb by up to 40 % and fall back over a run as the board
@@ -377,6 +378,29 @@ def wl_vendor_c2(dev):
     return wl
 
 
+def wl_vendor_conv(dev):
+    """Reference point, not this library: einconv's convolution the way the reference runs
+    it on a GPU (conv.py:153-207): the halo padded (F.pad), the input permuted to
+    (batch, channel, h, w), F.conv2d with padding 0 and the bias (MIOpen), the result
+    permuted back."""
+    wl = wl_conv(dev)
+
+    def call(es, xs):
+        x, w, b = xs
+        z = torch.nn.functional.pad(x, (0, 0, 1, 1, 1, 1)).permute(0, 3, 1, 2).contiguous()
+        return torch.nn.functional.conv2d(z, w, b, padding=0).permute(0, 2, 3, 1).contiguous()
+
+    wl.update(
+        key="vendor_conv",
+        workload=("reference: einconv's convolution as the reference runs it on a GPU "
+                  "(F.pad, permute, F.conv2d (MIOpen), permute), bf16"),
+        gpu_call=call,
+        kernel_name="F.pad + permute + F.conv2d (MIOpen) + permute",
+        cpu_call=lambda xs: call(None, xs),
+    )
+    return wl
+
+
 def _vendor_copy(wl, key, what):
     """Reference point, not this library: torch's own device copy (``Tensor.clone`` of a
     contiguous tensor, hipMemcpyAsync device to device) of the same bytes as ``wl``."""
@@ -414,6 +438,7 @@ WORKLOADS = {
     "vendor_c1": wl_vendor_c1,
     "vendor_c2": wl_vendor_c2,
     "vendor_c4": wl_vendor_c4,
+    "vendor_conv": wl_vendor_conv,
     "vendor_partition": wl_vendor_partition,
     "vendor_roll": wl_vendor_roll,
 }
@@ -779,7 +804,8 @@ def main(argv=None):
         line = measure_vs_vendor(es, args.workload, dev, args.steps, args.warmup, args.rounds)
         print(json.dumps(line), flush=True)
         return 0
-    calibration = ("copy", "dma_calib", "vendor_c1", "vendor_c2", "vendor_c4", "vendor_partition", "vendor_roll")
+    calibration = ("copy", "dma_calib", "vendor_c1", "vendor_c2", "vendor_c4", "vendor_conv", "vendor_partition",
+                   "vendor_roll")
     keys = [k for k in sorted(WORKLOADS) if k not in calibration] if args.workload == "all" else [args.workload]
     for key in keys:
         line = bench_one(es, key, dev, args.steps, args.warmup, cpu=not args.no_cpu)

@@ -14,7 +14,7 @@ def test_more_than_one_gpu_is_refused(capsys):
     assert "one GPU" in capsys.readouterr().err
 
 
-@pytest.mark.parametrize("key", ["c1", "c2", "c4"])
+@pytest.mark.parametrize("key", ["c1", "c2", "c4", "conv"])
 def test_paired_workloads_have_a_reference_point(key):
     # --vs-vendor times WORKLOADS[key] against WORKLOADS["vendor_" + key]
     assert key in bench.WORKLOADS and f"vendor_{key}" in bench.WORKLOADS
