@@ -15,10 +15,11 @@ es.einconv, the halo + convolution the reference runs through F.conv2d;
 permute and of einroll (benchmarks/bench_local.py, "large" size).  ``copy`` and
 ``dma_calib`` calibrate the traffic counters; ``vendor_c1``, ``vendor_c2`` and
 ``vendor_c4`` time torch's own GPU path (hipBLASLt) on configs 1, 2 and 4,
-``vendor_conv`` the reference's GPU path of einconv (F.pad, F.conv2d on MIOpen), and
+``vendor_conv`` the reference's GPU path of einconv (F.pad, F.conv2d on MIOpen),
+``vendor_c3`` and ``vendor_c5a``/``b``/``c`` its torch calls for configs 3 and 5, and
 ``vendor_partition`` and ``vendor_roll`` torch's own device copy of the same bytes
 as ``partition`` and ``roll``, as reference points.  ``all`` runs every workload but the calibrations and
-reference points.  ``--vs-vendor`` (with c1, c2, c4 or conv) times this library's launch and
+reference points.  ``--vs-vendor`` (with any workload that has a ``vendor_`` point) times this library's launch and
 the workload's reference point alternately on the same inputs, warm and flushed, the
 order swapped every round, so both see the same clock and power state of the board
 (dispatch times of either climb by up to 40 % and fall back over a run as the board
@@ -401,6 +402,35 @@ def wl_vendor_conv(dev):
     return wl
 
 
+def _vendor_torch(wl, key, what, call):
+    """Reference point, not this library: the workload the way the reference runs it on a
+    GPU, through torch's own kernels."""
+    wl.update(key=key, workload=f"reference: {what} (torch's own GPU kernels)", gpu_call=lambda es, xs: call(xs),
+              kernel_name=what, cpu_call=call)
+    return wl
+
+
+def wl_vendor_c3(dev):
+    # halo.py:402-418: F.pad, unfold along each windowed axis, permute, contiguous
+    def call(xs):
+        z = torch.nn.functional.pad(xs[0], (0, 0, 1, 1, 1, 1)).unfold(1, 3, 1).unfold(2, 3, 1)
+        return z.permute(0, 1, 2, 4, 5, 3).contiguous()  # b h w c kh kw -> b h w kh kw c
+
+    return _vendor_torch(wl_c3(dev), "vendor_c3", "F.pad + unfold + permute().contiguous()", call)
+
+
+def wl_vendor_c5a(dev):
+    return _vendor_torch(wl_c5a(dev), "vendor_c5a", "torch.sum over p", lambda xs: xs[0].sum(0))
+
+
+def wl_vendor_c5b(dev):
+    return _vendor_torch(wl_c5b(dev), "vendor_c5b", "torch.mul with broadcasting", lambda xs: xs[0] * xs[1])
+
+
+def wl_vendor_c5c(dev):
+    return _vendor_torch(wl_c5c(dev), "vendor_c5c", "torch.sum over n", lambda xs: xs[0].sum(1))
+
+
 def _vendor_copy(wl, key, what):
     """Reference point, not this library: torch's own device copy (``Tensor.clone`` of a
     contiguous tensor, hipMemcpyAsync device to device) of the same bytes as ``wl``."""
@@ -437,7 +467,11 @@ WORKLOADS = {
     "dma_calib": wl_dma_calib,
     "vendor_c1": wl_vendor_c1,
     "vendor_c2": wl_vendor_c2,
+    "vendor_c3": wl_vendor_c3,
     "vendor_c4": wl_vendor_c4,
+    "vendor_c5a": wl_vendor_c5a,
+    "vendor_c5b": wl_vendor_c5b,
+    "vendor_c5c": wl_vendor_c5c,
     "vendor_conv": wl_vendor_conv,
     "vendor_partition": wl_vendor_partition,
     "vendor_roll": wl_vendor_roll,
@@ -804,8 +838,7 @@ def main(argv=None):
         line = measure_vs_vendor(es, args.workload, dev, args.steps, args.warmup, args.rounds)
         print(json.dumps(line), flush=True)
         return 0
-    calibration = ("copy", "dma_calib", "vendor_c1", "vendor_c2", "vendor_c4", "vendor_conv", "vendor_partition",
-                   "vendor_roll")
+    calibration = ("copy", "dma_calib") + tuple(k for k in WORKLOADS if k.startswith("vendor_"))
     keys = [k for k in sorted(WORKLOADS) if k not in calibration] if args.workload == "all" else [args.workload]
     for key in keys:
         line = bench_one(es, key, dev, args.steps, args.warmup, cpu=not args.no_cpu)

@@ -14,7 +14,7 @@ def test_more_than_one_gpu_is_refused(capsys):
     assert "one GPU" in capsys.readouterr().err
 
 
-@pytest.mark.parametrize("key", ["c1", "c2", "c4", "conv"])
+@pytest.mark.parametrize("key", ["c1", "c2", "c3", "c4", "c5a", "c5b", "c5c", "conv"])
 def test_paired_workloads_have_a_reference_point(key):
     # --vs-vendor times WORKLOADS[key] against WORKLOADS["vendor_" + key]
     assert key in bench.WORKLOADS and f"vendor_{key}" in bench.WORKLOADS
@@ -23,6 +23,6 @@ def test_paired_workloads_have_a_reference_point(key):
 def test_paired_mode_needs_a_device_or_a_reference_point(capsys):
     # without a device the run stops before any timing; with one, a workload without a
     # vendor_ reference point is refused
-    assert bench.main(["--workload", "c3", "--vs-vendor"]) == 2
+    assert bench.main(["--workload", "copy", "--vs-vendor"]) == 2
     err = capsys.readouterr().err
     assert "no ROCm device" in err or "reference point" in err
