@@ -248,6 +248,17 @@ def test_fp32_64x64_kernels(gpu, m, n, k, layout):
     assert_rel(got, einshard_cpu("m k, n k -> m n", x, w), TOL[torch.float32])
 
 
+@pytest.mark.parametrize("m, n", [(200, 135), (130, 67), (33, 250)])
+def test_fp32_pipelined_kernel_element_stores(gpu, m, n):
+    # an N that is not a multiple of 4 (both operands K-contiguous): the pipelined fp32
+    # kernel writes the output one element at a time, the last column group partly
+    x = randn(m, 96, seed=m + 11)
+    w = randn(n, 96, seed=n + 13)
+    got = es.einshard("m k, n k -> m n", x.to(gpu), w.to(gpu))
+    assert _native.last_kernel() == "contract_f32_pipe_64x64", _native.last_kernel()
+    assert_rel(got, einshard_cpu("m k, n k -> m n", x, w), TOL[torch.float32])
+
+
 @pytest.mark.parametrize("w_layout", ["k", "n"])
 @pytest.mark.parametrize("case", ["two K levels", "two M sub-axes", "both"])
 def test_fp32_pipelined_kernel_walks(gpu, case, w_layout):
