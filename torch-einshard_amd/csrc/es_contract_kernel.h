@@ -1118,13 +1118,16 @@ struct PipeFrag<S, kMNContig> {
 // stages, filled by global_load_lds_dwordx4 copies issued a full K tile ahead.  With one
 // wave per SIMD nothing hides a stall, so the schedule is explicit, in program order (the
 // MFMAs are inline assembly, which the compiler's scheduling groups do not recognise):
-//   substep 0: its MFMAs, with the fragment reads of substep 1 spread evenly over them
-//              (issued all ahead of the MFMAs instead, they measured 2-5 % slower);
+//   substep 0: its MFMAs, with the fragment reads of substep 1 spread over the first
+//              three quarters of them, so that they have landed by the barrier's LDS
+//              wait (spread over all of them: about 1 % slower; issued all ahead of the
+//              MFMAs: 2-5 % slower);
 //   barrier:   K tile kt+1 has landed (own copies: vmcnt(0); everyone's: the barrier)
 //              and nobody reads stage kt any more;
-//   substep 1: its MFMAs, with the copies of K tile kt+2 into stage kt and the fragment
-//              reads of K tile kt+1's first substep spread evenly over them (bunching
-//              them measured 24 % slower: the copies and reads then queue on LDS).
+//   substep 1: its MFMAs, with the copies of K tile kt+2 into stage kt spread evenly
+//              over them and the fragment reads of K tile kt+1's first substep over
+//              their first three quarters (bunching them measured 24 % slower: the
+//              copies and reads then queue on LDS).
 // Blocks of 16 allow BN = 224 (waves of 128 x 112): an N extent of 7 x 256 = 1792 (one
 // tensor-parallel rank's share of a 14336-wide weight) then cuts into 8 tiles instead of
 // 7, and 16384 x 1792 into 512 tiles, two whole rounds of one tile per CU, where 256 x 256
@@ -1519,6 +1522,11 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
   constexpr int FM = WTM / 16, FN = WTN / 16;
   constexpr int STAGE = (BM + BN) * BK;
   constexpr int MMAS = FM * FN;  // per substep
+  // a substep's FM + FN fragment reads ride on its first three quarters of MFMAs, one per
+  // MFMA at most: read r goes out with MFMA q when read_slot(q) <= r < read_slot(q + 1)
+  constexpr int RQ = MMAS * 3 / 4;
+  static_assert(RQ >= FM + FN, "one fragment read per MFMA at most");
+  auto read_slot = [](int q) { return q >= RQ ? FM + FN : (q * (FM + FN)) / RQ; };
   using CopyA = std::conditional_t<
       HALO, PipeCopiesHalo<S, BM, WM * WN, G>,
       std::conditional_t<LA == kMNContig, PipeCopiesMN<S, BM, WM * WN, 0, G>, PipeCopies<S, BM, WM * WN, 0, G>>>;
@@ -1733,7 +1741,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
           const int c0 = (q * NI_D) / MMAS, c1 = ((q + 1) * NI_D) / MMAS;
           if (c0 != c1) copy_d(c0, d_far);
         }
-        const int r0 = (q * (FM + FN)) / MMAS, r1 = ((q + 1) * (FM + FN)) / MMAS;
+        const int r0 = read_slot(q), r1 = read_slot(q + 1);
         if (r0 != r1) {
           if (r0 < FM) af[1][r0] = fa.read(as, r0, 1);
           else bf[1][r0 - FM] = fb.read(bs, r0 - FM, 1);
@@ -1752,7 +1760,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
         // the other operand's tile kt + 2 into o_cur
         const int c0 = (q * NI_O) / MMAS, c1 = ((q + 1) * NI_O) / MMAS;
         if (c0 != c1) copy_o(c0, o_cur, other_off());
-        const int r0 = (q * (FM + FN)) / MMAS, r1 = ((q + 1) * (FM + FN)) / MMAS;
+        const int r0 = read_slot(q), r1 = read_slot(q + 1);
         if (r0 != r1) {
           if (r0 < FM) af[0][r0] = fa.read(an, r0, 0);
           else bf[0][r0 - FM] = fb.read(bn, r0 - FM, 0);
@@ -1803,7 +1811,7 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
       if constexpr (HALO) {
         if (q < CopyA::NI) hvoff[q] = ca.voff(q, tap);
       }
-      const int r0 = (q * (FM + FN)) / MMAS, r1 = ((q + 1) * (FM + FN)) / MMAS;
+      const int r0 = read_slot(q), r1 = read_slot(q + 1);
       if (r0 != r1) {
         if (r0 < FM) af[1][r0] = fa.read(stage_cur, r0, 1);
         else bf[1][r0 - FM] = fb.read(stage_cur + BM * BK, r0 - FM, 1);
@@ -1818,10 +1826,10 @@ __global__ __launch_bounds__(256, 1) void contract_pipe(const ContractArgs p) {
 #pragma unroll
     for (int q = 0; q < MMAS; ++q) {
       PipeMma<T>::mma(acc[q / FN][q % FN], bf[1][q % FN], af[1][q / FN]);
-      // copies and fragment reads spread evenly over the substep, alternating
+      // copies spread evenly over the substep, fragment reads over read_slot's window
       const int c0 = (q * NCOPY) / MMAS, c1 = ((q + 1) * NCOPY) / MMAS;
       if (c0 != c1) copy(c0, cur_addr);
-      const int r0 = (q * (FM + FN)) / MMAS, r1 = ((q + 1) * (FM + FN)) / MMAS;
+      const int r0 = read_slot(q), r1 = read_slot(q + 1);
       if (r0 != r1) {
         if (r0 < FM) af[0][r0] = fa.read(stage_nxt, r0, 0);
         else bf[0][r0 - FM] = fb.read(stage_nxt + BM * BK, r0 - FM, 0);
